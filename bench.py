@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the cuda_inf attention path on one MI355X.
+
+Default workload (the decode configuration of the headline metric): flash-
+decoding at 32768 tokens of context, 6 attention layers run back to back per
+token, batch 1, 32 query / 8 kv heads, head_dim 64, FP8 E4M3 group-64 cache
+with an fp16 tail.  Each timed step is one token: for every layer, append the
+fresh K/V through the tail (and the FP8 commit when a group fills) and run
+the attention.  Synthetic seeded inputs (N(0,1); K/V with 1% outliers x20;
+Q with QK-RMSNorm + RoPE), resident in HBM before timing starts.
+
+Printed: one JSON line with µs/token (warm: consecutive tokens; cold: the
+256 MB Infinity Cache flushed before every token), the decode kernel's
+roofline against 8 TB/s, a causal-prefill leg (4096 tokens), and the CPU
+oracle timed on this host as a baseline.
+
+    python bench.py [--steps 256] [--warmup 10] [--ctx 32768] [--layers 6]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+
+
+def algo_bytes(Tc: int, Tt: int) -> int:
+    """Algorithmic bytes of one layer's decode: FP8 K+V, fp16 group scales,
+    fp16 tail K+V, q in and out."""
+    return 1024 * Tc + (Tc // 64) * 8 * 2 * 2 + 2048 * Tt + 8192
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=6)
+    ap.add_argument("--nsplit", type=int, default=0,
+                    help="0: one-launch decode; >0: split+combine with this split count")
+    ap.add_argument("--cold-steps", type=int, default=32)
+    ap.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        sys.exit("bench.py measures one GPU: the attention path runs on a single MI355X; "
+                 "--gpus above 1 is not supported")
+
+    import torch
+    from cuda_inf_amd import _lib, workload
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd._lib import D, NH, NKV, call
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
+    total_steps = W + 2 * K + a.cold_steps
+    maxT = ctx + total_steps + 64
+    log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
+    log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
+
+    # ---- caches: ctx tokens per layer, loaded through the append loop
+    layers = []
+    for l in range(nL):
+        L = AttnLayer(maxT, nsplit=a.nsplit, device=dev)
+        g = workload.generator(1000 + l, dev)
+        for c0 in range(0, ctx, 8192):
+            n = min(8192, ctx - c0)
+            k = workload.with_outliers(workload.normal_f16((n, NKV, D), g, dev), g)
+            v = workload.with_outliers(workload.normal_f16((n, NKV, D), g, dev), g)
+            call("cia_layer_append", ctypes.byref(L._s), k.data_ptr(), v.data_ptr(), n, c0,
+                 stream.cuda_stream)
+        layers.append(L)
+    torch.cuda.synchronize()
+    assert all(L.committed == ctx - ctx % 64 for L in layers)
+    arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+
+    # ---- per-token inputs for every step and layer
+    g = workload.generator(7, dev)
+    pos = torch.arange(ctx, ctx + total_steps, device=dev)
+    q = workload.normal_f16((total_steps, nL, NH, D), g, dev)
+    q = torch.stack([workload.prep_qk(q[:, l], pos) for l in range(nL)], dim=1).contiguous()
+    kk = workload.with_outliers(workload.normal_f16((total_steps, nL, NKV, D), g, dev), g)
+    vv = workload.with_outliers(workload.normal_f16((total_steps, nL, NKV, D), g, dev), g)
+    out = torch.empty((total_steps, nL, NH, D), dtype=torch.float16, device=dev)
+    qrow, krow = nL * NH * D, nL * NKV * D
+    cur = {"step": 0}
+
+    def run(steps, events=None):
+        s0 = cur["step"]
+        call("cia_decode_loop", arr, nL, q.data_ptr() + s0 * qrow * 2,
+             kk.data_ptr() + s0 * krow * 2, vv.data_ptr() + s0 * krow * 2,
+             out.data_ptr() + s0 * qrow * 2, ctx + s0, steps, 0.125, events,
+             stream.cuda_stream)
+        cur["step"] += steps
+
+    def bytes_of_steps(s0, steps):
+        tot = 0
+        for i in range(s0, s0 + steps):
+            qp = ctx + i
+            Tc = ((qp + 1) // 64) * 64
+            tot += algo_bytes(Tc, qp + 1 - Tc)
+        return tot * nL
+
+    # ---- warm-up, then the timed region (warm: consecutive tokens)
+    run(W)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_timed = cur["step"]
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(K)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    warm_ms = e0.elapsed_time(e1)
+    us_tok = warm_ms * 1e3 / K
+    timed_bytes = bytes_of_steps(s_timed, K)
+    log(f"warm: {us_tok:.2f} us/token, effective {timed_bytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s")
+
+    # ---- per-kernel timing: events around each layer's attention launch
+    nev = 2 * K * nL
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(nev)]
+    for e in evs:  # the hipEvent_t handles exist once recorded
+        e.record(stream)
+    torch.cuda.synchronize()
+    ev_arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs]) if nev else None
+    s_k = cur["step"]
+    run(K, ev_arr)
+    torch.cuda.synchronize()
+    durs = [evs[2 * r].elapsed_time(evs[2 * r + 1]) for r in range(K * nL)]
+    kern_ms = sum(durs) / len(durs)
+    kern_bytes = bytes_of_steps(s_k, K) / (K * nL)
+    achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
+    log(f"decode kernel: {kern_ms * 1e3:.2f} us avg, {kern_bytes / 1e6:.2f} MB/launch, "
+        f"{achieved:.0f} GB/s")
+
+    # ---- cold: flush the Infinity Cache (write 1 GiB) before every token
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(a.cold_steps):
+        flush.fill_(1)
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        run(1)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(c0.elapsed_time(c1) * 1e3)
+    del flush
+    cold.sort()
+    cold_us = cold[len(cold) // 2] if cold else None
+    if cold:
+        log(f"cold: median {cold_us:.2f} us/token")
+    mean_tok_bytes = timed_bytes / K
+
+    # ---- prefill leg: causal attention_fused over a fresh cache
+    prefill = None
+    if a.prefill > 0:
+        S = a.prefill
+        Lp = AttnLayer(S + 64, nsplit=16, device=dev)
+        qp, kp, vp = workload.qkv(S, seed=0, device=dev)
+        Lp.forward(qp, kp, vp, 0)  # warm-up (appends + attends)
+        torch.cuda.synchronize()
+        from cuda_inf_amd import kernels as Kn
+        outp = torch.empty_like(qp)
+        reps = 3
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        for _ in range(reps):
+            Kn.attention_fused(qp, Lp.kc8, Lp.vc8, Lp.ksc, Lp.vsc, Lp.ktail, Lp.vtail,
+                               Lp.committed, outp, None, S, 0, 0.125)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        pms = p0.elapsed_time(p1) / reps
+        flops = 4.0 * D * NH * S * (S + 1) / 2
+        prefill = {"tokens": S, "us": round(pms * 1e3, 1),
+                   "tflops": round(flops / (pms * 1e-3) / 1e12, 2),
+                   "mfma_f16_frac": round(flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                   "kernel": "attention_fused"}
+        log(f"prefill {S}: {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s")
+
+    # ---- CPU baseline: the oracle on this host's cores, one layer at a time
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(layers[0], arr[0].committed, ctx + cur["step"] - 1, q, nL,
+                           a.cpu_seconds, log)
+
+    res = {
+        "metric": "decode-attn µs/token + HBM GB/s (% of 8 TB/s) at 32k ctx; prefill MFMA util",
+        "value": round(us_tok, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(warm_ms / K, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (fp8-e4m3/fp16 cache, f32 accumulate)",
+        "data": "synthetic: seeded N(0,1), K/V 1% outliers x20, Q QK-RMSNorm+RoPE",
+        "config": {"workload": f"flash-decoding, ctx {ctx}, {nL} attention layers/token, batch 1, "
+                               f"32Q/8KV heads, d64, FP8 E4M3 group-64 KV + fp16 tail",
+                   "context": ctx, "layers": nL, "decode": "one-launch" if a.nsplit == 0
+                   else f"split+combine nsplit={a.nsplit}"},
+        "effective_gbps_warm": round(timed_bytes / (warm_ms * 1e-3) / 1e9, 1),
+        "cold_us_per_token": round(cold_us, 3) if cold_us else None,
+        "effective_gbps_cold": round(mean_tok_bytes / (cold_us * 1e-6) / 1e9, 1) if cold_us else None,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_decode_fused", "algo_bytes_per_launch": int(kern_bytes),
+                     "avg_launch_us": round(kern_ms * 1e3, 3)},
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def cpu_baseline(L, committed, qpos, q, nL, seconds, log):
+    """The oracle's split+combine (16 splits, the reference's launch shape) on
+    one layer's cache copied to the host (keys 0..qpos); reported per token of
+    nL layers."""
+    import numpy as np
+    import torch
+    import oracle
+    ref = oracle.Group64Cache(L.maxT)
+    ref.kc8[:] = L.kc8.cpu().numpy()
+    ref.vc8[:] = L.vc8.cpu().numpy()
+    ref.ksc[:] = L.ksc.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref.vsc[:] = L.vsc.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref.ktail[:] = L.ktail.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref.vtail[:] = L.vtail.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref.committed = committed
+    qn = q[0, 0].cpu().view(torch.int16).numpy().view(np.uint16)
+    res = {}
+    ncores = min(os.cpu_count() or 1, 16)
+    for threads in (1, ncores):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attn_decode(qn, ref, qpos, nsplit=16, nthreads=threads)
+            n += 1
+            el = time.perf_counter() - t0
+            if el > seconds / 2:
+                break
+        res[threads] = el / n
+        log(f"cpu oracle, {threads} thread(s): {el / n * 1e3:.1f} ms per layer ({n} runs)")
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    best = min(res, key=res.get)
+    return {"value": round(res[best] * nL * 1e6, 1), "unit": "us/token", "cores": best,
+            "kind": "port",
+            "sample": f"oracle split+combine (16 splits), one layer at {qpos + 1} keys, "
+                      f"x{nL} layers; single-thread {res[1] * nL * 1e6:.0f} us/token; "
+                      f"host {model} ({os.cpu_count()} cpus)"}
+
+
+if __name__ == "__main__":
+    main()

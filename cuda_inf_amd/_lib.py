@@ -1,0 +1,115 @@
+"""Loader of libcuda_inf_attn.so (the gfx950 attention library) via ctypes.
+
+The library is built in-tree by ``make -C cuda_inf_amd/csrc`` (or
+``__graft_entry__.build()``).  There is no fallback: if the library is
+missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcuda_inf_attn.so")
+CSRC = os.path.join(HERE, "csrc")
+
+# Shapes (engine.cu:22-23, 35-38)
+NH, NKV, GQA, D, KVGROUP = 32, 8, 4, 64, 64
+NSPLIT_DEFAULT = 16
+NSPLIT_MAX = 4096
+
+STATUS = {0: "CIA_OK", 1: "CIA_ERR_NULL", 2: "CIA_ERR_ALIGN", 3: "CIA_ERR_ARG",
+          4: "CIA_ERR_HIP", 5: "CIA_ERR_STATE", 6: "CIA_ERR_NOSLOT"}
+
+# Every symbol include/cuda_inf_attn.h declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES = {
+    "cia_strerror": (ctypes.c_char_p, [_I]),
+    "cia_last_hip_error": (_I, []),
+    "cia_version": (ctypes.c_char_p, []),
+    "cia_e4m3_encode_range": (_I, [ctypes.c_uint32, ctypes.c_int64, _P, _P]),
+    "cia_kv_write_tail": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "cia_kv_commit_group": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "cia_attention_fused": (_I, [_P] * 7 + [_I, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_attn_decode_split": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I, _P]),
+    "cia_attn_decode_combine": (_I, [_P, _P, _P, _P, _I, _P]),
+    "cia_attn_decode": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, _P]),
+    "cia_decode_workspace_bytes": (ctypes.c_int64, []),
+    "cia_kv_quant_write": (_I, [_P] * 7 + [_I, _P]),
+    "cia_attention_h2o": (_I, [_P] * 6 + [_I, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_mass_workspace_bytes": (ctypes.c_int64, [_I]),
+    "cia_kv_append_plan": (_I, [_P, _I, _I, _P, _I, _P]),
+    "cia_h2o_clamp": (None, [_P, _P, _I, _I]),
+    "cia_h2o_pick_slots": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),
+    "cia_layer_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_layer_append": (_I, [_P, _P, _P, _I, _I, _P]),
+    "cia_decode_loop": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
+}
+
+
+class CiaError(RuntimeError):
+    def __init__(self, fn: str, code: int, lib):
+        msg = lib.cia_strerror(code).decode()
+        extra = ""
+        if code == 4:
+            extra = f" (hipError {lib.cia_last_hip_error()})"
+        super().__init__(f"{fn}: {STATUS.get(code, code)}: {msg}{extra}")
+        self.code = code
+
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the library with the Makefile in csrc/ (hipcc, gfx950)."""
+    args = ["make", "-s", "-C", CSRC, "-j8"]
+    if force:
+        args.append("-B")
+    subprocess.run(args, check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C {CSRC}` "
+                "(or __graft_entry__.build()); there is no non-HIP fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, code: int) -> None:
+    if code != 0:
+        raise CiaError(fn, code, lib())
+
+
+def call(fn: str, *args) -> None:
+    check(fn, getattr(lib(), fn)(*args))
+
+
+class cia_append_op(ctypes.Structure):
+    _fields_ = [("src_token", _I), ("slot", _I), ("cnt", _I), ("commit", _I),
+                ("commit_base", _I), ("commit_grp", _I)]
+
+
+class cia_layer(ctypes.Structure):
+    """Mirror of ``cia_layer`` in include/cuda_inf_attn.h."""
+    _fields_ = [
+        ("kc8", _P), ("vc8", _P), ("ksc", _P), ("vsc", _P), ("ktail", _P), ("vtail", _P),
+        ("maxT", _I), ("committed", _I),
+        ("nsplit", _I), ("pm", _P), ("pl", _P), ("po", _P), ("ws_decode", _P),
+        ("budget", _I), ("window", _I),
+        ("kf", _P), ("vf", _P), ("ks", _P), ("vs", _P), ("hattn", _P), ("d_slotpos", _P),
+        ("d_dst", _P), ("h_slotpos", _P), ("h_attn", _P), ("n_live", _I), ("ws_mass", _P),
+    ]

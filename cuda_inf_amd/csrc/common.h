@@ -1,0 +1,133 @@
+// common.h -- device helpers shared by the gfx950 kernels of the cuda_inf
+// attention path: fp16 / OCP-E4M3 conversions, the deterministic exp, wave64
+// reductions, and the status plumbing of the C-ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cuda_inf_attn.h"
+
+namespace cia {
+
+constexpr int NH = CIA_NH;
+constexpr int NKV = CIA_NKV;
+constexpr int GQA = CIA_GQA;
+constexpr int D = CIA_HEAD_DIM;
+constexpr int G = CIA_KVGROUP;
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------- status
+// Records the HIP error of the last failing call (per host thread).
+void set_hip_error(hipError_t e);
+// After a launch: CIA_ERR_HIP if the launch failed.
+int launch_status();
+
+#define CIA_REQUIRE(cond, code) \
+  do {                          \
+    if (!(cond)) return (code); \
+  } while (0)
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// ---------------------------------------------------------------- types
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- fp16
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+// round-to-nearest-even (the MODE register's default rounding)
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// ---------------------------------------------------------------- E4M3
+// gfx950's fp8 conversions use the OCP E4M3 format (bias 7, max 448,
+// S.1111.111 = NaN).  Decoding is exact.
+template <int kByte>
+__device__ __forceinline__ float e4m3_to_f32(uint32_t word) {
+  return __builtin_amdgcn_cvt_f32_fp8(word, kByte);
+}
+// bytes 0,1 (kHi = false) or 2,3 (kHi = true) of `word` -> two fp32
+template <bool kHi>
+__device__ __forceinline__ f32x2 e4m3x2_to_f32(uint32_t word) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8(word, kHi);
+}
+
+// Encode with SATFINITE: finite values and infinities beyond +-448 clamp to
+// +-448, NaN keeps its sign as S.1111.111; the hardware conversion rounds to
+// nearest even.
+__device__ __forceinline__ float sat448(float x) {
+  return __builtin_fminf(__builtin_fmaxf(x, -448.0f), 448.0f);
+}
+__device__ __forceinline__ uint32_t nan_code(float x) {
+  return ((__builtin_bit_cast(uint32_t, x) >> 24) & 0x80u) | 0x7Fu;
+}
+// packs e4m3(a) into byte 0 and e4m3(b) into byte 1
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
+  uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false) & 0xFFFFu;
+  if (__builtin_isnan(a)) r = (r & 0xFF00u) | nan_code(a);
+  if (__builtin_isnan(b)) r = (r & 0x00FFu) | (nan_code(b) << 8);
+  return r;
+}
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  return e4m3x2(a, b) | (e4m3x2(c, d) << 16);
+}
+
+// The quantisation scale of the reference, amax/448 + 1e-12 in fp32 with an
+// IEEE division (hipcc's default fp32 division is correctly rounded).
+__device__ __forceinline__ float quant_scale(float amax) {
+  return amax / 448.0f + 1e-12f;
+}
+
+// ---------------------------------------------------------------- exp
+// Deterministic exp used for the H2O attention mass: Cody-Waite reduction by
+// ln2 (two constants), degree-7 Taylor polynomial in Horner form with
+// explicit fma, exact power-of-two scale.  Inputs below -60 give 0.  Every
+// operation is a single IEEE-rounded op, so the result is bit-identical on
+// any IEEE-754 machine with the same sequence.
+__device__ __forceinline__ float exp_det(float x) {
+  if (!(x >= -60.0f)) return (x != x) ? x : 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  float kf = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-kf, 0.693145751953125f, x);
+  r = __builtin_fmaf(-kf, 1.428606765330187045e-06f, r);
+  float p = 1.98412701138295233249664306640625e-04f;
+  p = __builtin_fmaf(p, r, 1.38888892810791730880737304687500e-03f);
+  p = __builtin_fmaf(p, r, 8.33333376795053482055664062500000e-03f);
+  p = __builtin_fmaf(p, r, 4.16666679084300994873046875000000e-02f);
+  p = __builtin_fmaf(p, r, 1.66666671633720397949218750000000e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int k = (int)kf;
+  return p * __builtin_bit_cast(float, (uint32_t)(k + 127) << 23);
+}
+
+// fast exp for the tolerance-checked softmax (v_exp_f32 is exp2)
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
+}
+
+// ---------------------------------------------------------------- waves
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+  return v;
+}
+
+}  // namespace cia

@@ -1,0 +1,242 @@
+// decode.hip -- flash-decoding over the group-64 FP8 cache on gfx950
+// (engine.cu:386-480) and the fused causal prefill (engine.cu:236-308).
+//
+// The reference launches one block per (query head, split) and so reads
+// every K/V byte four times (once per query head of a GQA group).  Here a
+// workgroup owns (kv head, split) and serves all four query heads from one
+// read of each key row.  Split ranges are the reference's
+// ceil((qpos+1)/nsplit) so the partials keep its [h*nsplit+split] meaning.
+#include "attn_range.h"
+
+namespace cia {
+
+__device__ __forceinline__ void split_range(int total, int nsplit, int sp, int* a, int* b) {
+  const int chunk = (total + nsplit - 1) / nsplit;
+  const int ks = sp * chunk;
+  *a = ks;
+  *b = total < ks + chunk ? total : ks + chunk;
+}
+
+// grid = (8 kv heads, nsplit), block = 256
+__global__ __launch_bounds__(256) void k_decode_split(const uint16_t* __restrict__ q,
+                                                      Group64Cache c, int qpos, float scale,
+                                                      float* __restrict__ pm,
+                                                      float* __restrict__ pl,
+                                                      float* __restrict__ po, int nsplit) {
+  __shared__ float lds[kRangeLds];
+  __shared__ float sM[4], sL[4], sO[4 * D];
+  const int kvh = blockIdx.x, sp = blockIdx.y;
+  int a, b;
+  split_range(qpos + 1, nsplit, sp, &a, &b);
+  attend_range(q, c, kvh, scale, a, b, lds, sM, sL, sO);
+  const int j = threadIdx.x >> 6, d = threadIdx.x & 63;
+  const int pi = (kvh * GQA + j) * nsplit + sp;
+  po[(size_t)pi * D + d] = sO[j * D + d];
+  if (d == 0) {
+    pm[pi] = sM[j];
+    pl[pi] = sL[j];
+  }
+}
+
+// engine.cu:467-480 with runtime nsplit; grid = 32 heads, block = 64 dims
+__device__ __forceinline__ float combine_one(const float* pm, const float* pl, const float* po,
+                                             int h, int d, int nsplit) {
+  float gm = -1e30f;
+  for (int s = 0; s < nsplit; s++) gm = __builtin_fmaxf(gm, pm[h * nsplit + s]);
+  float l = 0.f, acc = 0.f;
+  for (int s = 0; s < nsplit; s++) {
+    const int pi = h * nsplit + s;
+    const float ls = pl[pi];
+    if (ls <= 0.f) continue;
+    const float w = fast_exp(pm[pi] - gm);
+    l = __builtin_fmaf(ls, w, l);
+    acc = __builtin_fmaf(po[(size_t)pi * D + d], w, acc);
+  }
+  return acc / l;
+}
+
+__global__ __launch_bounds__(64) void k_decode_combine(const float* __restrict__ pm,
+                                                       const float* __restrict__ pl,
+                                                       const float* __restrict__ po,
+                                                       uint16_t* __restrict__ out, int nsplit) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  out[h * D + d] = f2h(combine_one(pm, pl, po, h, d, nsplit));
+}
+
+// ---------------------------------------------------------------- one launch
+// Workspace of the one-launch decode: per-kv-head arrival counters, then the
+// partials of kMaxFusedSplits splits per query head.
+constexpr int kMaxFusedSplits = 256;
+constexpr size_t kWsCounters = 256;  // bytes (8 ints, padded)
+constexpr size_t kWsPm = kWsCounters;
+constexpr size_t kWsPl = kWsPm + sizeof(float) * NH * kMaxFusedSplits;
+constexpr size_t kWsPo = kWsPl + sizeof(float) * NH * kMaxFusedSplits;
+constexpr size_t kWsBytes = kWsPo + sizeof(float) * NH * kMaxFusedSplits * D;
+
+// split count of the one-launch decode: ~256 keys per workgroup
+static inline int fused_splits(int total) {
+  int ns = (total + 255) / 256;
+  return ns < 1 ? 1 : (ns > kMaxFusedSplits ? kMaxFusedSplits : ns);
+}
+
+// grid = (8, ns), block = 256.  The last workgroup of each kv head to
+// finish merges that head group's partials and re-arms its counter.
+__global__ __launch_bounds__(256) void k_decode_fused(const uint16_t* __restrict__ q,
+                                                      Group64Cache c, int qpos, float scale,
+                                                      uint16_t* __restrict__ out,
+                                                      char* __restrict__ ws, int ns) {
+  __shared__ float lds[kRangeLds];
+  __shared__ float sM[4], sL[4], sO[4 * D];
+  __shared__ int last;
+  int* counters = (int*)ws;
+  float* pm = (float*)(ws + kWsPm);
+  float* pl = (float*)(ws + kWsPl);
+  float* po = (float*)(ws + kWsPo);
+  const int kvh = blockIdx.x, sp = blockIdx.y;
+  int a, b;
+  split_range(qpos + 1, ns, sp, &a, &b);
+  attend_range(q, c, kvh, scale, a, b, lds, sM, sL, sO);
+  const int j = threadIdx.x >> 6, d = threadIdx.x & 63;
+  const int pi = (kvh * GQA + j) * ns + sp;
+  po[(size_t)pi * D + d] = sO[j * D + d];
+  if (d == 0) {
+    pm[pi] = sM[j];
+    pl[pi] = sL[j];
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last = (atomicAdd(&counters[kvh], 1) == ns - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // merge: wave j owns query head 4*kvh+j; the split weights go through LDS
+  // and every lane then reads its dim of all ns partials, 16 loads in flight
+  __shared__ float sw[4][kMaxFusedSplits];
+  const int h = kvh * GQA + j;
+  float gm = -1e30f;
+  for (int s = d; s < ns; s += 64) gm = __builtin_fmaxf(gm, pm[h * ns + s]);
+  gm = wave_max(gm);
+  float lsum = 0.f;
+  for (int s = d; s < ns; s += 64) {
+    const float ls = pl[h * ns + s];
+    const float w = ls > 0.f ? fast_exp(pm[h * ns + s] - gm) : 0.f;
+    sw[j][s] = w;
+    lsum = __builtin_fmaf(ls, w, lsum);
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();
+  const float* pr = po + (size_t)h * ns * D + d;
+  float acc[16];
+#pragma unroll
+  for (int u = 0; u < 16; u++) acc[u] = 0.f;
+  int s = 0;
+  for (; s + 16 <= ns; s += 16) {
+#pragma unroll
+    for (int u = 0; u < 16; u++) acc[u] = __builtin_fmaf(pr[(size_t)(s + u) * D], sw[j][s + u], acc[u]);
+  }
+  for (; s < ns; s++) acc[0] = __builtin_fmaf(pr[(size_t)s * D], sw[j][s], acc[0]);
+  float tot = 0.f;
+#pragma unroll
+  for (int u = 0; u < 16; u++) tot += acc[u];
+  out[h * D + d] = f2h(tot / lsum);
+  if (threadIdx.x == 0) atomicExch(&counters[kvh], 0);
+}
+
+// ---------------------------------------------------------------- prefill
+// attention_fused: grid = (S, 8 kv heads), block = 256; query i attends keys
+// [0, past+i] (FP8 below `committed`, tail above).
+__global__ __launch_bounds__(256) void k_prefill(const uint16_t* __restrict__ q, Group64Cache c,
+                                                 uint16_t* __restrict__ out, int past,
+                                                 float scale) {
+  __shared__ float lds[kRangeLds];
+  __shared__ float sM[4], sL[4], sO[4 * D];
+  const int i = blockIdx.x, kvh = blockIdx.y;
+  const uint16_t* qi = q + (size_t)i * NH * D;
+  attend_range(qi, c, kvh, scale, 0, past + i + 1, lds, sM, sL, sO);
+  const int j = threadIdx.x >> 6, d = threadIdx.x & 63;
+  out[((size_t)i * NH + kvh * GQA + j) * D + d] = f2h(sO[j * D + d] * (1.f / sL[j]));
+}
+
+}  // namespace cia
+
+using namespace cia;
+
+static int check_cache(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                       const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
+                       const uint16_t* vtail, int committed) {
+  CIA_REQUIRE(q && kc8 && vc8 && ksc && vsc && ktail && vtail, CIA_ERR_NULL);
+  CIA_REQUIRE(committed >= 0 && committed % G == 0, CIA_ERR_ARG);
+  CIA_REQUIRE(aligned(q, 16) && aligned(kc8, 16) && aligned(vc8, 16) && aligned(ktail, 16) &&
+                  aligned(vtail, 16) && aligned(ksc, 2) && aligned(vsc, 2),
+              CIA_ERR_ALIGN);
+  return CIA_OK;
+}
+
+extern "C" int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                                     const uint16_t* ksc, const uint16_t* vsc,
+                                     const uint16_t* ktail, const uint16_t* vtail, int committed,
+                                     int qpos, float scale, float* pm, float* pl, float* po,
+                                     int nsplit, void* stream) {
+  int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
+  if (st) return st;
+  CIA_REQUIRE(pm && pl && po, CIA_ERR_NULL);
+  CIA_REQUIRE(qpos >= 0 && nsplit >= 1 && nsplit <= CIA_NSPLIT_MAX, CIA_ERR_ARG);
+  CIA_REQUIRE(qpos - committed < G, CIA_ERR_STATE);  // the tail holds at most 64 keys
+  Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
+  hipLaunchKernelGGL(k_decode_split, dim3(NKV, nsplit), dim3(256), 0, (hipStream_t)stream, q, c,
+                     qpos, scale, pm, pl, po, nsplit);
+  return launch_status();
+}
+
+extern "C" int cia_attn_decode_combine(const float* pm, const float* pl, const float* po,
+                                       uint16_t* out, int nsplit, void* stream) {
+  CIA_REQUIRE(pm && pl && po && out, CIA_ERR_NULL);
+  CIA_REQUIRE(nsplit >= 1 && nsplit <= CIA_NSPLIT_MAX, CIA_ERR_ARG);
+  hipLaunchKernelGGL(k_decode_combine, dim3(NH), dim3(D), 0, (hipStream_t)stream, pm, pl, po,
+                     out, nsplit);
+  return launch_status();
+}
+
+extern "C" int64_t cia_decode_workspace_bytes(void) { return (int64_t)kWsBytes; }
+
+extern "C" int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                               const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
+                               const uint16_t* vtail, int committed, int qpos, float scale,
+                               uint16_t* out, void* ws, void* stream) {
+  int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
+  if (st) return st;
+  CIA_REQUIRE(out && ws, CIA_ERR_NULL);
+  CIA_REQUIRE(aligned(ws, 256), CIA_ERR_ALIGN);
+  CIA_REQUIRE(qpos >= 0, CIA_ERR_ARG);
+  CIA_REQUIRE(qpos - committed < G, CIA_ERR_STATE);
+  Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
+  const int ns = fused_splits(qpos + 1);
+  hipLaunchKernelGGL(k_decode_fused, dim3(NKV, ns), dim3(256), 0, (hipStream_t)stream, q, c, qpos,
+                     scale, out, (char*)ws, ns);
+  return launch_status();
+}
+
+// attn_sum support lives in mass.hip
+extern "C" __attribute__((visibility("hidden"))) int cia_mass_group64(const uint16_t* q, const uint8_t* kc8, const uint16_t* ksc,
+                                const uint16_t* ktail, int committed, float* attn_sum, int S,
+                                int past, float scale, void* ws, void* stream);
+
+extern "C" int cia_attention_fused(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                                   const uint16_t* ksc, const uint16_t* vsc,
+                                   const uint16_t* ktail, const uint16_t* vtail, int committed,
+                                   uint16_t* out, float* attn_sum, int S, int past, float scale,
+                                   void* ws, void* stream) {
+  CIA_REQUIRE(S >= 0 && past >= 0, CIA_ERR_ARG);
+  if (S == 0) return CIA_OK;
+  int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
+  if (st) return st;
+  CIA_REQUIRE(out, CIA_ERR_NULL);
+  CIA_REQUIRE(aligned(out, 2), CIA_ERR_ALIGN);
+  CIA_REQUIRE(past + S - 1 - committed < G, CIA_ERR_STATE);
+  Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
+  hipLaunchKernelGGL(k_prefill, dim3(S, NKV), dim3(256), 0, (hipStream_t)stream, q, c, out, past,
+                     scale);
+  st = launch_status();
+  if (st || !attn_sum) return st;
+  return cia_mass_group64(q, kc8, ksc, ktail, committed, attn_sum, S, past, scale, ws, stream);
+}

@@ -1,0 +1,278 @@
+// host.hip -- host side of the cuda_inf attention path: status codes, the
+// append planner (engine.cu:830-845), the H2O clamps and slot picker
+// (engine.cu:752-756, 808-823) and the attention branch of layer_forward
+// (engine.cu:802-857) driving the gfx950 kernels through the C-ABI.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <vector>
+
+#include "cuda_inf_attn.h"
+
+namespace cia {
+
+static thread_local int g_last_hip = 0;
+
+void set_hip_error(hipError_t e) { g_last_hip = (int)e; }
+
+int launch_status() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_hip_error(e);
+    return CIA_ERR_HIP;
+  }
+  return CIA_OK;
+}
+
+static int hip_check(hipError_t e) {
+  if (e != hipSuccess) {
+    set_hip_error(e);
+    return CIA_ERR_HIP;
+  }
+  return CIA_OK;
+}
+
+}  // namespace cia
+
+using namespace cia;
+
+extern "C" const char* cia_strerror(int status) {
+  switch (status) {
+    case CIA_OK: return "ok";
+    case CIA_ERR_NULL: return "required pointer is NULL";
+    case CIA_ERR_ALIGN: return "pointer is not aligned as required";
+    case CIA_ERR_ARG: return "integer argument out of range";
+    case CIA_ERR_HIP: return "HIP runtime call or kernel launch failed";
+    case CIA_ERR_STATE: return "cache state inconsistent (tail would exceed 64 tokens)";
+    case CIA_ERR_NOSLOT: return "H2O: no slot below 1e30 could be evicted";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int cia_last_hip_error(void) { return g_last_hip; }
+
+extern "C" const char* cia_version(void) { return "cuda_inf_attn 0.1 gfx950"; }
+
+// ---------------------------------------------------------------- append plan
+extern "C" int cia_kv_append_plan(int* committed, int S, int past, cia_append_op* ops,
+                                  int max_ops, int* n_ops) {
+  if (!committed || !n_ops || (!ops && S > 0)) return CIA_ERR_NULL;
+  if (S < 0 || past < 0 || *committed < 0 || *committed % CIA_KVGROUP) return CIA_ERR_ARG;
+  // the tail holds tokens committed..past-1, so past - committed in [0, 64)
+  if (past < *committed || past - *committed >= CIA_KVGROUP) return CIA_ERR_STATE;
+  int placed = 0, n = 0, c = *committed;
+  while (placed < S) {
+    const int gpos = past + placed;
+    const int slot = gpos - c;
+    const int can = std::min(S - placed, CIA_KVGROUP - slot);
+    if (n >= max_ops) return CIA_ERR_ARG;
+    cia_append_op& op = ops[n++];
+    op.src_token = placed;
+    op.slot = slot;
+    op.cnt = can;
+    placed += can;
+    op.commit = (slot + can == CIA_KVGROUP);
+    op.commit_base = c;
+    op.commit_grp = c / CIA_KVGROUP;
+    if (op.commit) c += CIA_KVGROUP;
+  }
+  *committed = c;
+  *n_ops = n;
+  return CIA_OK;
+}
+
+// ---------------------------------------------------------------- H2O policy
+extern "C" void cia_h2o_clamp(int* budget, int* window, int prompt_len, int maxT) {
+  if (*budget < prompt_len) *budget = prompt_len;
+  if (*budget > maxT) *budget = maxT;
+  if (*window <= 0) *window = *budget / 2;
+  if (*window >= *budget) *window = *budget - 1;
+}
+
+extern "C" int cia_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos, float* attn_host,
+                                  int S, int past, int32_t* dst, int32_t* zeroed) {
+  int evictions = 0;
+  for (int j = 0; j < S; j++) {
+    const int posj = past + j;
+    int slot;
+    if (zeroed) zeroed[j] = 0;
+    if (*n_live < C) {
+      slot = (*n_live)++;
+    } else {
+      int best = -1;
+      float bv = 1e30f;
+      for (int t = 0; t < C; t++)  // outside the window, strict <: lowest slot wins ties
+        if (slotpos[t] <= posj - W && attn_host[t] < bv) {
+          bv = attn_host[t];
+          best = t;
+        }
+      if (best < 0)
+        for (int t = 0; t < C; t++)
+          if (attn_host[t] < bv) {
+            bv = attn_host[t];
+            best = t;
+          }
+      if (best < 0) return -CIA_ERR_NOSLOT;
+      slot = best;
+      attn_host[slot] = 1e30f;  // never pick the same slot twice in one batch
+      if (zeroed) zeroed[j] = 1;
+      evictions++;
+    }
+    slotpos[slot] = posj;
+    dst[j] = slot;
+  }
+  return evictions;
+}
+
+// ---------------------------------------------------------------- layer driver
+namespace {
+
+__global__ void k_zero_picked(float* attn, const int32_t* dst, const int32_t* zero_flags, int S) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < S && zero_flags[j]) attn[dst[j]] = 0.0f;
+}
+
+int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                uint16_t* out, int S, int past, float scale, int* evicted, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  const int C = L->budget;
+  if (!L->kf || !L->vf || !L->ks || !L->vs || !L->hattn || !L->d_slotpos || !L->d_dst ||
+      !L->h_slotpos || !L->h_attn || !L->ws_mass)
+    return CIA_ERR_NULL;
+  // the reference fetches attn_sum only when a slot must be evicted
+  // (engine.cu:813-814); the fetch is a blocking copy
+  const bool will_evict = L->n_live + S > C;
+  if (will_evict) {
+    int st = hip_check(hipMemcpyAsync(L->h_attn, L->hattn, sizeof(float) * C,
+                                      hipMemcpyDeviceToHost, s));
+    if (st) return st;
+    st = hip_check(hipStreamSynchronize(s));
+    if (st) return st;
+  }
+  // dst and the zero flags travel in one H2D copy: d_dst[0..S), d_dst[S..2S)
+  static thread_local int32_t* hbuf = nullptr;
+  static thread_local int hcap = 0;
+  if (hcap < 2 * S) {
+    delete[] hbuf;
+    hbuf = new int32_t[2 * S];
+    hcap = 2 * S;
+  }
+  const int ev = cia_h2o_pick_slots(&L->n_live, C, L->window, L->h_slotpos, L->h_attn, S, past,
+                                    hbuf, hbuf + S);
+  if (ev < 0) return -ev;
+  if (evicted) *evicted = -1;
+  for (int j = 0; j < S && evicted; j++)
+    if (hbuf[S + j]) *evicted = hbuf[j];
+  int st = hip_check(hipMemcpyAsync(L->d_dst, hbuf, sizeof(int32_t) * 2 * S,
+                                    hipMemcpyHostToDevice, s));
+  if (st) return st;
+  st = hip_check(hipMemcpyAsync(L->d_slotpos, L->h_slotpos, sizeof(int32_t) * C,
+                                hipMemcpyHostToDevice, s));
+  if (st) return st;
+  // the host buffers are reused by the next call: wait for the copies
+  st = hip_check(hipStreamSynchronize(s));
+  if (st) return st;
+  if (ev > 0) {
+    hipLaunchKernelGGL(k_zero_picked, dim3((S + 255) / 256), dim3(256), 0, s, L->hattn, L->d_dst,
+                       L->d_dst + S, S);
+    if ((st = launch_status())) return st;
+  }
+  st = cia_kv_quant_write(k, v, L->kf, L->vf, L->ks, L->vs, L->d_dst, S, stream);
+  if (st) return st;
+  return cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out, L->hattn,
+                           S, past, scale, L->ws_mass, stream);
+}
+
+// placement loop (engine.cu:830-845): copy into the tail, commit full groups
+int group64_append(cia_layer* L, const uint16_t* k, const uint16_t* v, int S, int past,
+                   void* stream) {
+  if (past + S > L->maxT) return CIA_ERR_ARG;
+  cia_append_op small[4];
+  std::vector<cia_append_op> big;
+  cia_append_op* ops = small;
+  const int max_ops = S / CIA_KVGROUP + 2;
+  if (max_ops > 4) {
+    big.resize(max_ops);
+    ops = big.data();
+  }
+  int n = 0, committed = L->committed;
+  int st = cia_kv_append_plan(&committed, S, past, ops, max_ops, &n);
+  if (st) return st;
+  for (int i = 0; i < n; i++) {
+    const cia_append_op& op = ops[i];
+    const size_t off = (size_t)op.src_token * CIA_NKV * CIA_HEAD_DIM;
+    st = cia_kv_write_tail(k + off, v + off, L->ktail, L->vtail, op.slot, op.cnt, stream);
+    if (st) return st;
+    if (op.commit) {
+      st = cia_kv_commit_group(L->ktail, L->vtail, L->kc8, L->vc8, L->ksc, L->vsc,
+                               op.commit_base, op.commit_grp, stream);
+      if (st) return st;
+    }
+  }
+  L->committed = committed;
+  return CIA_OK;
+}
+
+int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int past, float scale,
+                   void* stream) {
+  if (S == 1) {
+    if (L->nsplit > 0) {
+      int st = cia_attn_decode_split(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail,
+                                     L->committed, past, scale, L->pm, L->pl, L->po, L->nsplit,
+                                     stream);
+      if (st) return st;
+      return cia_attn_decode_combine(L->pm, L->pl, L->po, out, L->nsplit, stream);
+    }
+    return cia_attn_decode(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
+                           past, scale, out, L->ws_decode, stream);
+  }
+  return cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
+                             out, nullptr, S, past, scale, nullptr, stream);
+}
+
+}  // namespace
+
+extern "C" int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t* k,
+                                 const uint16_t* v, uint16_t* out, int S, int past, float scale,
+                                 int* evicted, void* stream) {
+  if (!L || !q || !k || !v || !out) return CIA_ERR_NULL;
+  if (S < 1 || past < 0) return CIA_ERR_ARG;
+  if (evicted) *evicted = -1;
+  if (L->budget > 0) return h2o_forward(L, q, k, v, out, S, past, scale, evicted, stream);
+  int st = group64_append(L, k, v, S, past, stream);
+  if (st) return st;
+  return group64_attend(L, q, out, S, past, scale, stream);
+}
+
+extern "C" int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t* v, int S,
+                                int past, void* stream) {
+  if (!L || !k || !v) return CIA_ERR_NULL;
+  if (S < 0 || past < 0) return CIA_ERR_ARG;
+  if (L->budget > 0) return CIA_ERR_STATE;  // H2O layers place tokens by policy
+  return S ? group64_append(L, k, v, S, past, stream) : CIA_OK;
+}
+
+extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
+                               const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
+                               int steps, float scale, void** events, void* stream) {
+  if (!layers || !q || !k || !v || !out) return CIA_ERR_NULL;
+  if (n_layers < 1 || steps < 0 || past < 0) return CIA_ERR_ARG;
+  for (int l = 0; l < n_layers; l++)
+    if (layers[l].budget > 0) return CIA_ERR_STATE;
+  const size_t qrow = (size_t)CIA_NH * CIA_HEAD_DIM, krow = (size_t)CIA_NKV * CIA_HEAD_DIM;
+  hipStream_t s = (hipStream_t)stream;
+  for (int i = 0; i < steps; i++) {
+    for (int l = 0; l < n_layers; l++) {
+      const size_t r = (size_t)i * n_layers + l;
+      cia_layer* L = &layers[l];
+      int st = group64_append(L, k + r * krow, v + r * krow, 1, past + i, stream);
+      if (st) return st;
+      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r], s)))) return st;
+      st = group64_attend(L, q + r * qrow, out + r * qrow, 1, past + i, scale, stream);
+      if (st) return st;
+      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r + 1], s)))) return st;
+    }
+  }
+  return CIA_OK;
+}

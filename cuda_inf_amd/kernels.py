@@ -1,0 +1,142 @@
+"""The reference engine's attention kernels as Python calls on torch tensors.
+
+Each function keeps the name, argument order and meaning of one kernel of
+g023/cuda_inf ``src/engine.cu`` and runs the gfx950 implementation through the
+C-ABI of libcuda_inf_attn.so on torch's current stream.  fp16 tensors may be
+``torch.float16`` or ``torch.int16``/``torch.uint16`` bit patterns.  Errors
+raise ``CiaError``; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import D, KVGROUP, NH, NKV, NSPLIT_DEFAULT, call
+
+_F16 = (torch.float16, torch.int16, torch.uint16)
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtypes=None, numel=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if dtypes is not None and t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name}: needs at least {numel} elements, has {t.numel()}")
+    return t.data_ptr()
+
+
+def _opt(t, name, dtypes=None, numel=None):
+    return None if t is None else _dev(t, name, dtypes, numel)
+
+
+def e4m3_encode_range(first_bits: int, n: int, out) -> None:
+    """Device E4M3 encoder on the fp32 bit patterns first_bits .. first_bits+n-1."""
+    call("cia_e4m3_encode_range", first_bits, n, _dev(out, "out", (torch.uint8,), n), _stream())
+
+
+# ------------------------------------------------------------ group-64 cache
+def kv_write_tail(k, v, ktail, vtail, slot: int, cnt: int) -> None:
+    """engine.cu:190-198: tail rows slot..slot+cnt-1 <- k, v [cnt, 8, 64]."""
+    n = cnt * NKV * D
+    call("cia_kv_write_tail", _dev(k, "k", _F16, n), _dev(v, "v", _F16, n),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         slot, cnt, _stream())
+
+
+def kv_commit_group(ktail, vtail, kc8, vc8, ksc, vsc, dst_tok_base: int, grp: int) -> None:
+    """engine.cu:202-228: commit the full tail group to FP8 with fp16 scales."""
+    call("cia_kv_commit_group", _dev(ktail, "ktail", _F16, KVGROUP * NKV * D),
+         _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         _dev(kc8, "kc8", (torch.uint8,), (dst_tok_base + KVGROUP) * NKV * D),
+         _dev(vc8, "vc8", (torch.uint8,), (dst_tok_base + KVGROUP) * NKV * D),
+         _dev(ksc, "ksc", _F16, (grp + 1) * NKV), _dev(vsc, "vsc", _F16, (grp + 1) * NKV),
+         dst_tok_base, grp, _stream())
+
+
+# ------------------------------------------------------------ attention
+def attention_fused(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out, attn_sum,
+                    S: int, past: int, scale: float, ws=None) -> None:
+    """engine.cu:236-308: causal attention of S queries at past..past+S-1."""
+    T = past + S
+    call("cia_attention_fused", _dev(q, "q", _F16, S * NH * D),
+         _dev(kc8, "kc8", (torch.uint8,), min(T, committed) * NKV * D),
+         _dev(vc8, "vc8", (torch.uint8,), min(T, committed) * NKV * D),
+         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         committed, _dev(out, "out", _F16, S * NH * D),
+         _opt(attn_sum, "attn_sum", (torch.float32,), T), S, past, float(scale),
+         _opt(ws, "ws", None, mass_workspace_bytes(S) if attn_sum is not None else None),
+         _stream())
+
+
+def attn_decode_split(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int,
+                      scale: float, pm, pl, po, nsplit: int = NSPLIT_DEFAULT) -> None:
+    """engine.cu:396-464 with a runtime split count."""
+    call("cia_attn_decode_split", _dev(q, "q", _F16, NH * D),
+         _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
+         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         committed, qpos, float(scale),
+         _dev(pm, "pm", (torch.float32,), NH * nsplit), _dev(pl, "pl", (torch.float32,), NH * nsplit),
+         _dev(po, "po", (torch.float32,), NH * nsplit * D), nsplit, _stream())
+
+
+def attn_decode_combine(pm, pl, po, out, nsplit: int = NSPLIT_DEFAULT) -> None:
+    """engine.cu:467-480 with a runtime split count."""
+    call("cia_attn_decode_combine", _dev(pm, "pm", (torch.float32,), NH * nsplit),
+         _dev(pl, "pl", (torch.float32,), NH * nsplit),
+         _dev(po, "po", (torch.float32,), NH * nsplit * D), _dev(out, "out", _F16, NH * D),
+         nsplit, _stream())
+
+
+def decode_workspace_bytes() -> int:
+    return int(_lib.lib().cia_decode_workspace_bytes())
+
+
+def new_decode_workspace(device="cuda") -> torch.Tensor:
+    """Zero-filled workspace of the one-launch decode (its counters start at 0)."""
+    return torch.zeros(decode_workspace_bytes(), dtype=torch.uint8, device=device)
+
+
+def attn_decode(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int, scale: float,
+                out, ws) -> None:
+    """Flash-decoding in one launch (replaces engine.cu:848-852's two launches)."""
+    call("cia_attn_decode", _dev(q, "q", _F16, NH * D),
+         _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
+         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         committed, qpos, float(scale), _dev(out, "out", _F16, NH * D),
+         _dev(ws, "ws", (torch.uint8,), decode_workspace_bytes()), _stream())
+
+
+# ------------------------------------------------------------ H2O
+def kv_quant_write(k, v, kf, vf, ks, vs, dst_slots, S: int) -> None:
+    """engine.cu:317-333: per-token FP8 quantisation into slots dst_slots[j]."""
+    call("cia_kv_quant_write", _dev(k, "k", _F16, S * NKV * D), _dev(v, "v", _F16, S * NKV * D),
+         _dev(kf, "kf", (torch.uint8,)), _dev(vf, "vf", (torch.uint8,)),
+         _dev(ks, "ks", _F16), _dev(vs, "vs", _F16),
+         _dev(dst_slots, "dst_slots", (torch.int32,), S), S, _stream())
+
+
+def mass_workspace_bytes(S: int) -> int:
+    return int(_lib.lib().cia_mass_workspace_bytes(S))
+
+
+def attention_h2o(q, kf, vf, ks, vs, slot_pos, n_live: int, out, attn_sum, S: int, past: int,
+                  scale: float, ws) -> None:
+    """engine.cu:337-384 with the deterministic attention-mass rule."""
+    call("cia_attention_h2o", _dev(q, "q", _F16, S * NH * D),
+         _dev(kf, "kf", (torch.uint8,), n_live * NKV * D), _dev(vf, "vf", (torch.uint8,), n_live * NKV * D),
+         _dev(ks, "ks", _F16, n_live * NKV), _dev(vs, "vs", _F16, n_live * NKV),
+         _dev(slot_pos, "slot_pos", (torch.int32,), n_live), n_live,
+         _dev(out, "out", _F16, S * NH * D), _dev(attn_sum, "attn_sum", (torch.float32,), n_live),
+         S, past, float(scale), _dev(ws, "ws", None, mass_workspace_bytes(S)), _stream())

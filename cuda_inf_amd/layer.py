@@ -1,0 +1,138 @@
+"""One attention layer of the cuda_inf engine: its device cache, the host state
+the reference keeps beside it, and the attention branch of ``layer_forward``
+(engine.cu:802-857), run by the C++ driver ``cia_layer_forward``.
+
+Also exposes the host-only policy helpers (append planner, H2O clamps and
+slot picker) which need no GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import D, KVGROUP, NH, NKV, NSPLIT_DEFAULT, call, cia_append_op, cia_layer
+from .kernels import decode_workspace_bytes, mass_workspace_bytes
+
+
+# ------------------------------------------------------------ host policy
+def kv_append_plan(committed: int, S: int, past: int):
+    """engine.cu:830-845 as a list of ops; returns (ops, new_committed)."""
+    max_ops = S // KVGROUP + 2
+    ops = (cia_append_op * max_ops)()
+    c = ctypes.c_int(committed)
+    n = ctypes.c_int(0)
+    call("cia_kv_append_plan", ctypes.byref(c), S, past, ops, max_ops, ctypes.byref(n))
+    out = [dict(src_token=o.src_token, slot=o.slot, cnt=o.cnt, commit=bool(o.commit),
+                commit_base=o.commit_base, commit_grp=o.commit_grp) for o in ops[:n.value]]
+    return out, c.value
+
+
+def h2o_clamp(budget: int, window: int, prompt_len: int, maxT: int):
+    """engine.cu:752-756; returns (budget, window)."""
+    b, w = ctypes.c_int(budget), ctypes.c_int(window)
+    _lib.lib().cia_h2o_clamp(ctypes.byref(b), ctypes.byref(w), prompt_len, maxT)
+    return b.value, w.value
+
+
+def h2o_pick_slots(n_live: int, C: int, W: int, slotpos: np.ndarray, attn_host: np.ndarray,
+                   S: int, past: int):
+    """engine.cu:808-823 on host arrays (updated in place).
+
+    Returns (n_live, dst[S], zeroed[S], evictions)."""
+    assert slotpos.dtype == np.int32 and attn_host.dtype == np.float32
+    dst = np.zeros(S, np.int32)
+    zeroed = np.zeros(S, np.int32)
+    nl = ctypes.c_int(n_live)
+    ev = _lib.lib().cia_h2o_pick_slots(ctypes.byref(nl), C, W, slotpos.ctypes.data,
+                                       attn_host.ctypes.data, S, past, dst.ctypes.data,
+                                       zeroed.ctypes.data)
+    if ev < 0:
+        _lib.check("cia_h2o_pick_slots", -ev)
+    return nl.value, dst, zeroed, ev
+
+
+# ------------------------------------------------------------ the layer
+class AttnLayer:
+    """Device buffers of one attention layer (engine.cu:596-613, 731-770).
+
+    ``nsplit`` > 0 runs the reference's two-launch flash-decoding with that
+    split count; ``nsplit`` = 0 runs the one-launch decode.  ``budget`` > 0
+    enables H2O eviction with a ``budget``-slot buffer and local ``window``
+    (0 -> budget/2, clamped as the reference does against ``prompt_len``).
+    """
+
+    def __init__(self, max_tokens: int, *, nsplit: int = NSPLIT_DEFAULT, budget: int = 0,
+                 window: int = 0, prompt_len: int = 0, max_batch: int = 4096,
+                 device="cuda"):
+        dev = torch.device(device)
+        self.device = dev
+        self.maxT = max_tokens
+        u8, f16, f32, i32 = torch.uint8, torch.float16, torch.float32, torch.int32
+        ng = max_tokens // KVGROUP + 2
+        self.kc8 = torch.zeros((max_tokens, NKV, D), dtype=u8, device=dev)
+        self.vc8 = torch.zeros((max_tokens, NKV, D), dtype=u8, device=dev)
+        self.ksc = torch.zeros((ng, NKV), dtype=f16, device=dev)
+        self.vsc = torch.zeros((ng, NKV), dtype=f16, device=dev)
+        self.ktail = torch.zeros((KVGROUP, NKV, D), dtype=f16, device=dev)
+        self.vtail = torch.zeros((KVGROUP, NKV, D), dtype=f16, device=dev)
+        self.nsplit = nsplit
+        ns = max(nsplit, 1)
+        self.pm = torch.zeros(NH * ns, dtype=f32, device=dev)
+        self.pl = torch.zeros(NH * ns, dtype=f32, device=dev)
+        self.po = torch.zeros(NH * ns * D, dtype=f32, device=dev)
+        self.ws_decode = torch.zeros(decode_workspace_bytes(), dtype=u8, device=dev)
+        s = cia_layer()
+        for name in ("kc8", "vc8", "ksc", "vsc", "ktail", "vtail", "pm", "pl", "po", "ws_decode"):
+            setattr(s, name, getattr(self, name).data_ptr())
+        s.maxT, s.committed, s.nsplit = max_tokens, 0, nsplit
+        self.budget = 0
+        if budget > 0:
+            budget, window = h2o_clamp(budget, window, prompt_len, max_tokens)
+            self.budget, self.window = budget, window
+            C = budget
+            self.kf = torch.zeros((C, NKV, D), dtype=u8, device=dev)
+            self.vf = torch.zeros((C, NKV, D), dtype=u8, device=dev)
+            self.ks = torch.zeros((C, NKV), dtype=f16, device=dev)
+            self.vs = torch.zeros((C, NKV), dtype=f16, device=dev)
+            self.hattn = torch.zeros(C, dtype=f32, device=dev)
+            self.d_slotpos = torch.full((C,), -1, dtype=i32, device=dev)
+            self.d_dst = torch.zeros(2 * max_batch, dtype=i32, device=dev)
+            self.h_slotpos = torch.full((C,), -1, dtype=i32).pin_memory()
+            self.h_attn = torch.zeros(C, dtype=f32).pin_memory()
+            self.ws_mass = torch.zeros(max(mass_workspace_bytes(max_batch), 8), dtype=u8, device=dev)
+            s.budget, s.window = budget, window
+            for name in ("kf", "vf", "ks", "vs", "hattn", "d_slotpos", "d_dst", "h_slotpos",
+                         "h_attn", "ws_mass"):
+                setattr(s, name, getattr(self, name).data_ptr())
+            s.n_live = 0
+        self.max_batch = max_batch
+        self._s = s
+
+    @property
+    def committed(self) -> int:
+        return self._s.committed
+
+    @property
+    def n_live(self) -> int:
+        return self._s.n_live
+
+    def forward(self, q, k, v, past: int, out=None, scale: float = 0.125):
+        """Append k, v [S,8,64] at positions past.. and attend q [S,32,64].
+
+        Returns (out [S,32,64] fp16, evicted slot of the last token or -1)."""
+        S = k.shape[0]
+        if self.budget and S > self.max_batch:
+            raise ValueError(f"S={S} exceeds max_batch={self.max_batch}")
+        for t, name, n in ((q, "q", S * NH * D), (k, "k", S * NKV * D), (v, "v", S * NKV * D)):
+            if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous() or t.numel() != n:
+                raise ValueError(f"{name}: need a contiguous device fp16 tensor of {n} elements")
+        if out is None:
+            out = torch.empty((S, NH, D), dtype=torch.float16, device=self.device)
+        ev = ctypes.c_int(-1)
+        call("cia_layer_forward", ctypes.byref(self._s), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+             out.data_ptr(), S, past, float(scale), ctypes.byref(ev),
+             torch.cuda.current_stream().cuda_stream)
+        return out, ev.value

@@ -1,0 +1,271 @@
+/*
+ * cuda_inf_attn.h -- C-ABI of the MI355X (gfx950) attention path of the
+ * cuda_inf engine: FP8 E4M3 group-64 KV cache, flash-decoding, fused causal
+ * prefill and H2O eviction.
+ *
+ * Every kernel entry point replaces one __global__ kernel of the reference
+ * engine (g023/cuda_inf, src/engine.cu) and keeps its parameter order and
+ * pointer roles, so a caller that launched
+ *     kernel<<<grid, block>>>(args...)
+ * calls
+ *     cia_kernel(args..., stream)
+ * instead.  The reference's launch site of each kernel is cited beside it.
+ *
+ * Conventions
+ *   - fp16 tensors are passed as uint16_t* (IEEE binary16 bit patterns).
+ *   - All pointers are device pointers owned by the caller (hipMalloc'd),
+ *     except where "host" is stated.  No entry point allocates device
+ *     memory or synchronises: every call is enqueued on `stream`
+ *     (a hipStream_t; NULL is the null stream).
+ *   - Every entry point returns CIA_OK (0) or a cia_status code; none calls
+ *     exit().  cia_strerror() names the code; after CIA_ERR_HIP,
+ *     cia_last_hip_error() returns the hipError_t of the failing call.
+ *   - Calls touching the same cache must be serialised by the caller (same
+ *     stream, or events), exactly as the reference's single stream does.
+ *
+ * Shapes are the reference's compile-time constants (engine.cu:22-23, 35-38).
+ * Cache layout of one attention layer (engine.cu:596-613, 731-770):
+ *     kc8, vc8       uint8  [maxT][CIA_NKV][CIA_HEAD_DIM]   committed FP8
+ *     ksc, vsc       fp16   [maxT/64 + 2][CIA_NKV]          group scales
+ *     ktail, vtail   fp16   [CIA_KVGROUP][CIA_NKV][CIA_HEAD_DIM]
+ *     attn_sum       f32    [maxT]
+ *   H2O slot buffer:
+ *     kf, vf         uint8  [C][CIA_NKV][CIA_HEAD_DIM]
+ *     ks, vs         fp16   [C][CIA_NKV]
+ *     slot_pos       int32  [C]           attn_sum  f32 [C]
+ *   Flash-decoding partials: pm, pl f32 [CIA_NH*nsplit],
+ *     po f32 [CIA_NH*nsplit][CIA_HEAD_DIM], index h*nsplit + split.
+ */
+#ifndef CUDA_INF_ATTN_H
+#define CUDA_INF_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CIA_NH 32            /* query heads            (engine.cu:36) */
+#define CIA_NKV 8            /* kv heads               (engine.cu:37) */
+#define CIA_GQA 4            /* query heads per kv head (engine.cu:38) */
+#define CIA_HEAD_DIM 64      /* (engine.cu:35) */
+#define CIA_KVGROUP 64       /* tokens per FP8 group   (engine.cu:23) */
+#define CIA_E4M3_MAX 448.0f  /* (engine.cu:22) */
+#define CIA_NSPLIT_DEFAULT 16   /* the reference's NSPLIT (engine.cu:392) */
+#define CIA_NSPLIT_MAX 4096
+
+typedef enum cia_status {
+  CIA_OK = 0,
+  CIA_ERR_NULL = 1,       /* a required pointer is NULL */
+  CIA_ERR_ALIGN = 2,      /* a pointer is not aligned as documented */
+  CIA_ERR_ARG = 3,        /* an integer argument is out of range */
+  CIA_ERR_HIP = 4,        /* a HIP runtime call or launch failed */
+  CIA_ERR_STATE = 5,      /* host-side cache state is inconsistent */
+  CIA_ERR_NOSLOT = 6      /* H2O: no slot could be chosen for eviction */
+} cia_status;
+
+const char* cia_strerror(int status);
+int cia_last_hip_error(void);
+/* version of this library, e.g. "cuda_inf_attn 0.1 gfx950" */
+const char* cia_version(void);
+
+/* ------------------------------------------------------------------ */
+/* group-64 FP8 KV cache                                              */
+/* ------------------------------------------------------------------ */
+
+/* kv_write_tail (engine.cu:190-198; launch engine.cu:838).
+ * Copies cnt fresh tokens k,v [cnt][8][64] into tail rows slot..slot+cnt-1.
+ * Requires 0 <= slot, 0 <= cnt, slot + cnt <= 64. */
+int cia_kv_write_tail(const uint16_t* k, const uint16_t* v, uint16_t* ktail,
+                      uint16_t* vtail, int slot, int cnt, void* stream);
+
+/* kv_commit_group (engine.cu:202-228; launch engine.cu:841-842).
+ * Per kv head: amax over the 64x64 tail block, scale = amax/448 + 1e-12
+ * (fp32), ksc/vsc[grp*8+h] = fp16(scale), FP8 bytes of x/scale into rows
+ * dst_tok_base..dst_tok_base+63.  Bytes and scales are bit-exact. */
+int cia_kv_commit_group(const uint16_t* ktail, const uint16_t* vtail,
+                        uint8_t* kc8, uint8_t* vc8, uint16_t* ksc,
+                        uint16_t* vsc, int dst_tok_base, int grp,
+                        void* stream);
+
+/* The device E4M3 encoder of f2e4m3 (engine.cu:24-26) that the commit and
+ * H2O writers use, exposed for validation: out[i] = e4m3(float bits
+ * first_bits + i) for i < n (no kernel counterpart in the reference). */
+int cia_e4m3_encode_range(uint32_t first_bits, int64_t n, uint8_t* out,
+                          void* stream);
+
+/* ------------------------------------------------------------------ */
+/* attention over the group-64 cache                                  */
+/* ------------------------------------------------------------------ */
+
+/* attention_fused (engine.cu:236-308; launch engine.cu:854-855).
+ * Causal attention for S queries q [S][32][64] at positions past..past+S-1
+ * over FP8 keys [0, min(committed, qpos+1)) and tail keys up to qpos.
+ * out [S][32][64] fp16.  attn_sum (may be NULL): per-key attention mass is
+ * added with the deterministic rule of cia_attention_h2o; it then needs
+ * `ws` of cia_mass_workspace_bytes(S) bytes (else ws may be NULL). */
+int cia_attention_fused(const uint16_t* q, const uint8_t* kc8,
+                        const uint8_t* vc8, const uint16_t* ksc,
+                        const uint16_t* vsc, const uint16_t* ktail,
+                        const uint16_t* vtail, int committed, uint16_t* out,
+                        float* attn_sum, int S, int past, float scale,
+                        void* ws, void* stream);
+
+/* attn_decode_split (engine.cu:396-464; launch engine.cu:848-851).
+ * One query (q row 0, [32][64]) at position qpos; keys [0, qpos] are cut
+ * into nsplit ranges of ceil((qpos+1)/nsplit) keys, as the reference does
+ * per query head.  Writes the partial softmax state (m, l, o) of every
+ * (query head, split) to pm/pl/po at index h*nsplit + split.  An empty
+ * split writes m = -1e30, l = 0.  nsplit in [1, CIA_NSPLIT_MAX]
+ * (the reference fixes 16). */
+int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
+                          const uint8_t* vc8, const uint16_t* ksc,
+                          const uint16_t* vsc, const uint16_t* ktail,
+                          const uint16_t* vtail, int committed, int qpos,
+                          float scale, float* pm, float* pl, float* po,
+                          int nsplit, void* stream);
+
+/* attn_decode_combine (engine.cu:467-480; launch engine.cu:852).
+ * Merges the nsplit partials of every query head into out [32][64] fp16;
+ * splits with l <= 0 are skipped. */
+int cia_attn_decode_combine(const float* pm, const float* pl, const float* po,
+                            uint16_t* out, int nsplit, void* stream);
+
+/* Flash-decoding in one launch (no counterpart kernel in the reference; it
+ * replaces the pair of launches at engine.cu:848-852).  Same result as
+ * cia_attn_decode_split followed by cia_attn_decode_combine with the
+ * workspace's own split count.  ws: cia_decode_workspace_bytes() bytes of
+ * device memory, zero-filled once before first use (the kernel leaves its
+ * counters at zero again after every call). */
+int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                    const uint16_t* ksc, const uint16_t* vsc,
+                    const uint16_t* ktail, const uint16_t* vtail,
+                    int committed, int qpos, float scale, uint16_t* out,
+                    void* ws, void* stream);
+int64_t cia_decode_workspace_bytes(void);
+
+/* ------------------------------------------------------------------ */
+/* H2O eviction                                                       */
+/* ------------------------------------------------------------------ */
+
+/* kv_quant_write (engine.cu:317-333; launch engine.cu:826).
+ * Per (token j, kv head h): scale = amax over 64 dims / 448 + 1e-12,
+ * FP8 bytes into kf/vf row dst_slots[j] (device int32 [S]),
+ * ks/vs[dst_slots[j]*8+h] = fp16(scale).  Bit-exact. */
+int cia_kv_quant_write(const uint16_t* k, const uint16_t* v, uint8_t* kf,
+                       uint8_t* vf, uint16_t* ks, uint16_t* vs,
+                       const int32_t* dst_slots, int S, void* stream);
+
+/* attention_h2o (engine.cu:337-384; launch engine.cu:827-828).
+ * Attention of S queries over the n_live slots whose slot_pos <= qpos;
+ * out [S][32][64] fp16.  attn_sum[t] (device f32, required as in the
+ * reference) gains the attention mass of every (query, head) with the
+ * deterministic rule below, so that the eviction order is reproducible:
+ *   s(t) = fma chain over d ascending of q[d]*k(t)[d] from 0, times scale;
+ *   m = max s; e = expdet(s - m); l = 64-lane strided sums, then a
+ *   butterfly; p = e * (1/l); attn_sum[t] += p in (query, head) order.
+ * ws: cia_mass_workspace_bytes(S) bytes of device scratch. */
+int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uint8_t* vf,
+                      const uint16_t* ks, const uint16_t* vs,
+                      const int32_t* slot_pos, int n_live, uint16_t* out,
+                      float* attn_sum, int S, int past, float scale, void* ws,
+                      void* stream);
+int64_t cia_mass_workspace_bytes(int S);
+
+/* ------------------------------------------------------------------ */
+/* host-side policy (plain C++, no device access)                     */
+/* ------------------------------------------------------------------ */
+
+/* One step of the reference's append loop (engine.cu:830-845). */
+typedef struct cia_append_op {
+  int src_token;    /* first fresh token of this op (offset into k/v) */
+  int slot;         /* tail slot it lands in */
+  int cnt;          /* tokens copied */
+  int commit;       /* 1 if the group fills and is committed after the copy */
+  int commit_base;  /* dst_tok_base of that commit (== committed before it) */
+  int commit_grp;   /* grp of that commit */
+} cia_append_op;
+
+/* Plans the append of S tokens at positions past..past+S-1 given
+ * *committed; fills ops[0..*n_ops) (max_ops entries available) and advances
+ * *committed.  Requires committed % 64 == 0 and
+ * committed <= past <= committed + 64 (the tail holds past-committed
+ * tokens).  Returns CIA_ERR_ARG / CIA_ERR_STATE on violations. */
+int cia_kv_append_plan(int* committed, int S, int past, cia_append_op* ops,
+                       int max_ops, int* n_ops);
+
+/* The reference's H2O clamps (engine.cu:752-756): budget >= prompt,
+ * budget <= maxT, window defaults to budget/2, window <= budget-1. */
+void cia_h2o_clamp(int* budget, int* window, int prompt_len, int maxT);
+
+/* H2O slot choice for S fresh tokens (engine.cu:808-823), on host arrays:
+ * slotpos[C] and *n_live are updated; attn_host[C] is the host copy of the
+ * device attention mass (picked slots are overwritten with 1e30 as the
+ * reference does).  dst[S] receives the slot of each token, zeroed[S]
+ * (may be NULL) 1 where that slot's device attn_sum must be cleared.
+ * Returns the number of evictions (>= 0) or -CIA_ERR_NOSLOT. */
+int cia_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos,
+                       float* attn_host, int S, int past, int32_t* dst,
+                       int32_t* zeroed);
+
+/* ------------------------------------------------------------------ */
+/* layer driver: the attention branch of layer_forward (engine.cu:802-857) */
+/* ------------------------------------------------------------------ */
+
+/* Device buffers of one attention layer (caller-owned, engine.cu:596-613)
+ * plus the host state the reference keeps beside them (committed[l],
+ * n_live[l], slotpos_h[l]). */
+typedef struct cia_layer {
+  /* group-64 cache */
+  uint8_t* kc8; uint8_t* vc8; uint16_t* ksc; uint16_t* vsc;
+  uint16_t* ktail; uint16_t* vtail;
+  int maxT;
+  int committed;
+  /* flash-decoding */
+  int nsplit;            /* 0 -> fused one-launch decode with ws_decode */
+  float* pm; float* pl; float* po;
+  void* ws_decode;       /* cia_decode_workspace_bytes() */
+  /* H2O (budget > 0 enables it) */
+  int budget, window;
+  uint8_t* kf; uint8_t* vf; uint16_t* ks; uint16_t* vs;
+  float* hattn;          /* device attn_sum [budget] */
+  int32_t* d_slotpos;    /* device [budget] */
+  int32_t* d_dst;        /* device [max tokens per call] */
+  int32_t* h_slotpos;    /* host [budget] */
+  float* h_attn;         /* host scratch [budget] */
+  int n_live;
+  void* ws_mass;         /* cia_mass_workspace_bytes(max tokens per call) */
+} cia_layer;
+
+/* Append S fresh tokens (k, v: device fp16 [S][8][64]) then attend q
+ * (device fp16 [S][32][64]) into out, exactly as engine.cu:802-857:
+ * H2O when budget > 0, else append + (S == 1 ? flash-decoding : fused).
+ * H2O mode performs the reference's blocking copies (engine.cu:814,
+ * 824-825) on `stream`.  On return *evicted (may be NULL) holds the slot
+ * evicted for the last token, or -1. */
+int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t* k,
+                      const uint16_t* v, uint16_t* out, int S, int past,
+                      float scale, int* evicted, void* stream);
+
+/* The placement loop alone (engine.cu:830-845): append S tokens at
+ * past..past+S-1 to the group-64 cache, committing every group that fills;
+ * no attention.  Used to load a context into the cache. */
+int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t* v,
+                     int S, int past, void* stream);
+
+/* The decode loop of the reference (engine.cu:954-958) restricted to the
+ * attention branches: for step s in [0, steps) and layer l in [0, n_layers)
+ * runs cia_layer_forward(&layers[l], q[s][l], k[s][l], v[s][l],
+ * out[s][l], 1, past + s, ...).  q/out: fp16 [steps][n_layers][32][64],
+ * k/v: fp16 [steps][n_layers][8][64].  events (may be NULL): 2*steps*n_layers
+ * hipEvent_t recorded before and after each layer's attention launch(es)
+ * (after the append), for per-kernel timing.  Group-64 layers only. */
+int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
+                    const uint16_t* k, const uint16_t* v, uint16_t* out,
+                    int past, int steps, float scale, void** events,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

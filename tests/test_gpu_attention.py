@@ -1,0 +1,153 @@
+"""GPU parity of the attention kernels against the oracle (tolerance
+2e-3 abs + 1e-3 rel of the fp32 oracle output).
+
+Flash-decoding split/combine (engine.cu:396-480), the one-launch decode, and
+attention_fused (engine.cu:236-308) on the group-64 FP8 cache.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _build(dev, orc, ntok, seed, outliers=False, nsplit=16):
+    """Cache holding ntok tokens (positions 0..ntok-1), built identically on
+    the GPU (AttnLayer's append loop) and in the oracle."""
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    L = AttnLayer(ntok + 64, nsplit=nsplit, device=dev)
+    ref = orc.Group64Cache(ntok + 64)
+    q, k, v = qkv(ntok, seed=seed, device="cpu", outliers=outliers)
+    kd, vd = k.to(dev), v.to(dev)
+    # append without attention: plan on host and run the writers
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.layer import kv_append_plan
+    ops, c = kv_append_plan(0, ntok, 0)
+    for op in ops:
+        s0 = op["src_token"]
+        K.kv_write_tail(kd[s0:], vd[s0:], L.ktail, L.vtail, op["slot"], op["cnt"])
+        if op["commit"]:
+            K.kv_commit_group(L.ktail, L.vtail, L.kc8, L.vc8, L.ksc, L.vsc, op["commit_base"],
+                              op["commit_grp"])
+    L._s.committed = c
+    ref.append(_u16(k), _u16(v), 0)
+    assert ref.committed == c
+    return L, ref, q
+
+
+def _decode_q(seed, qpos):
+    from cuda_inf_amd.workload import qkv
+    q, _, _ = qkv(1, seed=seed, device="cpu", past=qpos)
+    return q
+
+
+def test_decode_config0(orc, cia, dev):
+    """31 committed groups + 48-token tail (2032 keys), nsplit 16."""
+    from cuda_inf_amd import kernels as K
+    L, ref, _ = _build(dev, orc, 2032, seed=0)
+    assert L.committed == 1984
+    q = _decode_q(1, 2031)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    K.attn_decode_split(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, 1984, 2031, 0.125,
+                        L.pm, L.pl, L.po, 16)
+    K.attn_decode_combine(L.pm, L.pl, L.po, out, 16)
+    torch.cuda.synchronize()
+    _, r32, (pm, pl, po) = orc.attn_decode(_u16(q), ref, 2031, nsplit=16)
+    assert_close_f16(_u16(out), r32)
+    # partials: same split ranges as the reference
+    gm = L.pm.cpu().numpy()
+    np.testing.assert_allclose(gm, pm, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(L.pl.cpu().numpy(), pl, rtol=2e-4)
+    np.testing.assert_allclose(L.po.cpu().numpy().reshape(po.shape), po, rtol=2e-3, atol=2e-3)
+    # and the fused prefill's last row on the same cache gives the same answer
+    f16, f32 = orc.attention_fused(_u16(q), ref, 1, 2031)
+    np.testing.assert_allclose(f32[0], r32, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("nsplit", [1, 16, 64, 256, 512, 4096])
+def test_decode_nsplit_sweep(orc, cia, dev, nsplit):
+    from cuda_inf_amd import kernels as K
+    L, ref, _ = _build(dev, orc, 1000, seed=3, outliers=True)
+    q = _decode_q(4, 999)
+    pm = torch.zeros(32 * nsplit, device=dev)
+    pl = torch.zeros(32 * nsplit, device=dev)
+    po = torch.zeros(32 * nsplit * 64, device=dev)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    K.attn_decode_split(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed, 999,
+                        0.125, pm, pl, po, nsplit)
+    K.attn_decode_combine(pm, pl, po, out, nsplit)
+    torch.cuda.synchronize()
+    _, r32, (rpm, rpl, _) = orc.attn_decode(_u16(q), ref, 999, nsplit=nsplit, nthreads=8)
+    assert_close_f16(_u16(out), r32)
+    # empty splits: l == 0 and m == -1e30 exactly where the oracle has them
+    empty = rpl == 0
+    assert np.array_equal(pl.cpu().numpy() == 0, empty)
+    assert np.all(pm.cpu().numpy()[empty] == np.float32(-1e30))
+
+
+@pytest.mark.parametrize("ntok", [1, 63, 64, 65, 2032, 5000])
+def test_decode_one_launch(orc, cia, dev, ntok):
+    from cuda_inf_amd import kernels as K
+    L, ref, _ = _build(dev, orc, ntok, seed=ntok, outliers=True)
+    ws = K.new_decode_workspace(dev)
+    q = _decode_q(ntok + 1, ntok - 1)
+    _, r32, _ = orc.attn_decode(_u16(q), ref, ntok - 1, nsplit=16, nthreads=8)
+    for rep in range(3):  # the counters re-arm themselves
+        out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+        K.attn_decode(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed,
+                      ntok - 1, 0.125, out, ws)
+        torch.cuda.synchronize()
+        assert_close_f16(_u16(out), r32, what=f"rep {rep}")
+    assert int(ws[:32].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("S,past", [(1, 0), (333, 0), (64, 0), (50, 100), (130, 64), (700, 0)])
+def test_attention_fused(orc, cia, dev, S, past):
+    """Prefill through the layer driver (append, then fused attention)."""
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    L = AttnLayer(past + S + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(past + S + 64)
+    if past:
+        q0, k0, v0 = qkv(past, seed=7, device="cpu")
+        L.forward(q0.to(dev), k0.to(dev), v0.to(dev), 0)
+        ref.append(_u16(k0), _u16(v0), 0)
+    q, k, v = qkv(S, seed=8, device="cpu", past=past)
+    out, _ = L.forward(q.to(dev), k.to(dev), v.to(dev), past)
+    ref.append(_u16(k), _u16(v), past)
+    torch.cuda.synchronize()
+    if S == 1:
+        _, r32, _ = orc.attn_decode(_u16(q), ref, past, nsplit=16)
+        r32 = r32[None]
+    else:
+        _, r32 = orc.attention_fused(_u16(q), ref, S, past)
+    assert_close_f16(_u16(out), r32)
+
+
+def test_decode_steps_through_commit(orc, cia, dev):
+    """Decode steps that cross a group boundary (tail fills, commit, new tail)."""
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    n0 = 4000
+    L = AttnLayer(n0 + 200, nsplit=0, device=dev)  # one-launch decode
+    ref = orc.Group64Cache(n0 + 200)
+    q0, k0, v0 = qkv(n0, seed=11, device="cpu", outliers=True)
+    L.forward(q0.to(dev), k0.to(dev), v0.to(dev), 0)
+    ref.append(_u16(k0), _u16(v0), 0)
+    for step in range(100):
+        pos = n0 + step
+        q, k, v = qkv(1, seed=1000 + step, device="cpu", past=pos, outliers=True)
+        out, _ = L.forward(q.to(dev), k.to(dev), v.to(dev), pos)
+        ref.append(_u16(k), _u16(v), pos)
+        if step % 9 == 0 or pos % 64 in (62, 63, 0, 1):
+            torch.cuda.synchronize()
+            _, r32, _ = orc.attn_decode(_u16(q), ref, pos, nsplit=16, nthreads=8)
+            assert_close_f16(_u16(out)[0], r32, what=f"step {step} pos {pos}")
+    assert L.committed == ref.committed
