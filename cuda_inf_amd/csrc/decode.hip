@@ -63,85 +63,6 @@ __global__ __launch_bounds__(64) void k_decode_combine(const float* __restrict__
   out[h * D + d] = f2h(combine_one(pm, pl, po, h, d, nsplit));
 }
 
-// ---------------------------------------------------------------- one launch
-// Workspace of the one-launch decode: per-kv-head arrival counters, then the
-// partials of kMaxFusedSplits splits per query head.
-constexpr int kMaxFusedSplits = 256;
-constexpr size_t kWsCounters = 256;  // bytes (8 ints, padded)
-constexpr size_t kWsPm = kWsCounters;
-constexpr size_t kWsPl = kWsPm + sizeof(float) * NH * kMaxFusedSplits;
-constexpr size_t kWsPo = kWsPl + sizeof(float) * NH * kMaxFusedSplits;
-constexpr size_t kWsBytes = kWsPo + sizeof(float) * NH * kMaxFusedSplits * D;
-
-// split count of the one-launch decode: ~256 keys per workgroup
-static inline int fused_splits(int total) {
-  int ns = (total + 255) / 256;
-  return ns < 1 ? 1 : (ns > kMaxFusedSplits ? kMaxFusedSplits : ns);
-}
-
-// grid = (8, ns), block = 256.  The last workgroup of each kv head to
-// finish merges that head group's partials and re-arms its counter.
-__global__ __launch_bounds__(256) void k_decode_fused(const uint16_t* __restrict__ q,
-                                                      Group64Cache c, int qpos, float scale,
-                                                      uint16_t* __restrict__ out,
-                                                      char* __restrict__ ws, int ns) {
-  __shared__ float lds[kRangeLds];
-  __shared__ float sM[4], sL[4], sO[4 * D];
-  __shared__ int last;
-  int* counters = (int*)ws;
-  float* pm = (float*)(ws + kWsPm);
-  float* pl = (float*)(ws + kWsPl);
-  float* po = (float*)(ws + kWsPo);
-  const int kvh = blockIdx.x, sp = blockIdx.y;
-  int a, b;
-  split_range(qpos + 1, ns, sp, &a, &b);
-  attend_range(q, c, kvh, scale, a, b, lds, sM, sL, sO);
-  const int j = threadIdx.x >> 6, d = threadIdx.x & 63;
-  const int pi = (kvh * GQA + j) * ns + sp;
-  po[(size_t)pi * D + d] = sO[j * D + d];
-  if (d == 0) {
-    pm[pi] = sM[j];
-    pl[pi] = sL[j];
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = (atomicAdd(&counters[kvh], 1) == ns - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // merge: wave j owns query head 4*kvh+j; the split weights go through LDS
-  // and every lane then reads its dim of all ns partials, 16 loads in flight
-  __shared__ float sw[4][kMaxFusedSplits];
-  const int h = kvh * GQA + j;
-  float gm = -1e30f;
-  for (int s = d; s < ns; s += 64) gm = __builtin_fmaxf(gm, pm[h * ns + s]);
-  gm = wave_max(gm);
-  float lsum = 0.f;
-  for (int s = d; s < ns; s += 64) {
-    const float ls = pl[h * ns + s];
-    const float w = ls > 0.f ? fast_exp(pm[h * ns + s] - gm) : 0.f;
-    sw[j][s] = w;
-    lsum = __builtin_fmaf(ls, w, lsum);
-  }
-  lsum = wave_sum(lsum);
-  __syncthreads();
-  const float* pr = po + (size_t)h * ns * D + d;
-  float acc[16];
-#pragma unroll
-  for (int u = 0; u < 16; u++) acc[u] = 0.f;
-  int s = 0;
-  for (; s + 16 <= ns; s += 16) {
-#pragma unroll
-    for (int u = 0; u < 16; u++) acc[u] = __builtin_fmaf(pr[(size_t)(s + u) * D], sw[j][s + u], acc[u]);
-  }
-  for (; s < ns; s++) acc[0] = __builtin_fmaf(pr[(size_t)s * D], sw[j][s], acc[0]);
-  float tot = 0.f;
-#pragma unroll
-  for (int u = 0; u < 16; u++) tot += acc[u];
-  out[h * D + d] = f2h(tot / lsum);
-  if (threadIdx.x == 0) atomicExch(&counters[kvh], 0);
-}
-
 // ---------------------------------------------------------------- prefill
 // attention_fused: grid = (S, 8 kv heads), block = 256; query i attends keys
 // [0, past+i] (FP8 below `committed`, tail above).
@@ -197,23 +118,24 @@ extern "C" int cia_attn_decode_combine(const float* pm, const float* pl, const f
   return launch_status();
 }
 
-extern "C" int64_t cia_decode_workspace_bytes(void) { return (int64_t)kWsBytes; }
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
+    const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
+    int64_t ws_bytes, void* stream);
 
 extern "C" int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                                const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
                                const uint16_t* vtail, int committed, int qpos, float scale,
-                               uint16_t* out, void* ws, void* stream) {
+                               uint16_t* out, void* ws, int64_t ws_bytes, void* stream) {
   int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
   if (st) return st;
   CIA_REQUIRE(out && ws, CIA_ERR_NULL);
-  CIA_REQUIRE(aligned(ws, 256), CIA_ERR_ALIGN);
-  CIA_REQUIRE(qpos >= 0, CIA_ERR_ARG);
-  CIA_REQUIRE(qpos - committed < G, CIA_ERR_STATE);
-  Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
-  const int ns = fused_splits(qpos + 1);
-  hipLaunchKernelGGL(k_decode_fused, dim3(NKV, ns), dim3(256), 0, (hipStream_t)stream, q, c, qpos,
-                     scale, out, (char*)ws, ns);
-  return launch_status();
+  CIA_REQUIRE(aligned(ws, 16) && aligned(out, 2), CIA_ERR_ALIGN);
+  CIA_REQUIRE(qpos >= 0 && ws_bytes >= 0, CIA_ERR_ARG);
+  CIA_REQUIRE(committed <= qpos + 1 && qpos - committed < G, CIA_ERR_STATE);
+  return cia_decode_mfma(q, kc8, vc8, ksc, vsc, (uint16_t*)ktail, (uint16_t*)vtail, nullptr,
+                         nullptr, committed, qpos, scale, out, ws, ws_bytes, stream);
 }
 
 // attn_sum support lives in mass.hip

@@ -1,0 +1,371 @@
+// decode_mfma.hip -- flash-decoding of one query over the group-64 FP8 cache
+// on gfx950 matrix cores (replaces the pair attn_decode_split ->
+// attn_decode_combine, engine.cu:386-480, for the library's own split; the
+// fresh token's tail write, engine.cu:190-198, rides along).  Two launches:
+//
+// k_decode_attend covers the committed FP8 keys.  They are cut into "pairs":
+// 32 keys (half a 64-key group) x 4 kv heads (one half of the 8).  The pairs
+// of a half are spread evenly over the 8*nwg waves of its nwg workgroups; a
+// wave takes one pair per round and two waves share a SIMD, so one computes
+// while the other waits for memory.
+//   Loads: every 16-byte global load of a wave covers 4 keys x one 256-byte
+//     half-row, so each 16 lanes read 256 contiguous bytes.  K and V land in
+//     per-wave LDS tiles [32 keys][16 chunks of 16 B] with an XOR swizzle of
+//     the chunk index so the MFMA-layout reads below are conflict-free.
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = K (lane l: key l & 15 of a
+//     16-key tile, kv head l >> 4, 8 dims, read as 16 bytes per two MFMAs and
+//     converted fp8 -> fp16 exactly); B = Q^T block-diagonal over the 4 kv
+//     heads, so all 16 output columns (4 kv heads x 4 query heads) are real.
+//     Lane l = 16b + 4a + j then holds keys 4b..4b+3 (+16 per tile) of
+//     column (a, j).
+//   Online softmax per round in registers (scale folded in, log2 units).
+//   O = P V, block-diagonal with the kv head of k-group b rotated per MFMA
+//     (sigma_mu(b) = (b + mu) & 3) so each lane's P registers are its A
+//     operand as they stand (zero when its kv head is not sigma_mu(b)).  V
+//     comes back from LDS through ds_read_b64_tr_b8: 8 keys of one dim per
+//     lane.  Each pair's V scale multiplies its own PV product.
+//   The waves merge in LDS into one partial (m in log2 units, l, o[64]) per
+//   query head of the half.
+// k_decode_finish: one single-wave workgroup per item (query head, 8 dims).
+//   It issues every load at once -- the head's FP8 partials and the fp16 tail
+//   (keys committed..qpos; the fresh token is read from knew/vnew and written
+//   into the tail) -- then merges them and writes its 8 output values.
+//   (Workgroup-to-workgroup synchronisation inside one launch costs more on
+//   this part than a kernel boundary, hence the second launch.)
+#include "attn_range.h"
+
+namespace cia {
+
+constexpr int kDecWaves = 8;        // waves per workgroup
+constexpr int kMaxWgPerHalf = 128;  // at most one workgroup per CU of a 256-CU part
+constexpr int kPart = 4 + D;        // m (log2 units), l, 2 unused, o[64]: 16-byte rows
+constexpr int kItems = NH * 8;      // merge items: (query head, 8 dims)
+constexpr float kLog2e = 1.44269504088896340736f;
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+
+__device__ __forceinline__ f16x8 cvt8(uint32_t w0, uint32_t w1) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// LDS tile offsets: 32 keys x 256 bytes, chunk c (16 B, 0..15) of key k.
+// K: the 16 keys of a tile read the same logical chunk -> XOR with key & 15.
+// V: the 8 keys {4b..4b+3, 16+4b..16+4b+3} of one transposed read
+//    share a logical chunk -> XOR with a 3-bit function distinct on them.
+__device__ __forceinline__ int kaddr(int key, int c) { return key * 256 + ((c ^ (key & 15)) << 4); }
+__device__ __forceinline__ int vswz(int key) { return (key & 3) | (((key >> 4) & 1) << 2); }
+__device__ __forceinline__ int vaddr(int key, int c) { return key * 256 + ((c ^ vswz(key)) << 4); }
+
+struct DecodeArgs {
+  const uint16_t* q;  // [32][64]
+  const uint8_t* kc8;
+  const uint8_t* vc8;
+  const uint16_t* ksc;
+  const uint16_t* vsc;
+  uint16_t* ktail;
+  uint16_t* vtail;
+  const uint16_t* knew;  // fresh token [8][64] (key qpos), or null: it is in the tail
+  const uint16_t* vnew;
+  int committed, qpos;
+  float scale;
+  float* part;    // [32][nwg][kPart]: m, l, -, -, o[64]
+  int npairs;     // committed / 32
+  int nwg;        // workgroups per half
+  uint16_t* out;  // [32][64]
+};
+
+// ---------------------------------------------------------------- attend
+// grid = (nwg, 2 halves), block = 64 * kDecWaves
+__global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t klds[kDecWaves][32 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t vlds[kDecWaves][32 * 256];
+  __shared__ float sm[kDecWaves][16], sl[kDecWaves][16];
+  const int half = blockIdx.y;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int n = l & 15, b = l >> 4;  // MFMA column / k-group of this lane
+  uint8_t* kw = klds[w];
+  uint8_t* vw = vlds[w];
+  // this wave's pairs: an even share of the half's pairs
+  const int nwaves = a.nwg * kDecWaves;
+  const int wid = blockIdx.x * kDecWaves + w;
+  const int p0 = (int)(((long long)wid * a.npairs) / nwaves);
+  const int p1 = (int)(((long long)(wid + 1) * a.npairs) / nwaves);
+  // Q^T as the block-diagonal B operand, fp16
+  f16x8 qop[8];
+  if ((n >> 2) == b) {
+    const uint16_t* qp = a.q + (size_t)(half * 16 + n) * D;
+#pragma unroll
+    for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qp + 8 * mu);
+  } else {
+#pragma unroll
+    for (int mu = 0; mu < 8; mu++) qop[mu] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  const float qscale = a.scale * kLog2e;
+  float mx = -1e30f, lsum = 0.f;  // column (a, j) = n: running max (log2) and sum
+  f32x4 O[4];                     // rows (kv head b, query head i), dims 16 nu + n
+#pragma unroll
+  for (int v = 0; v < 4; v++) O[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int p = p0; p < p1; p++) {
+    const int kbase = p * 32;
+    // ---- loads: instruction i covers keys 4i..4i+3, lane -> (key 4i + b, chunk n)
+    u32x4 kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const size_t off = (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16;
+      kr[i] = *(const u32x4*)(a.kc8 + off);
+      vr[i] = *(const u32x4*)(a.vc8 + off);
+    }
+    // K scale of this lane's column kv head (times scale*log2e), V scale of
+    // this lane's row kv head
+    const int grp = kbase >> 6;
+    const float ksc = h2f(a.ksc[grp * NKV + half * 4 + (n >> 2)]) * qscale;
+    const float vsc = h2f(a.vsc[grp * NKV + half * 4 + b]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) *(u32x4*)(kw + kaddr(4 * i + b, n)) = kr[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) *(u32x4*)(vw + vaddr(4 * i + b, n)) = vr[i];
+    // ---- S^T = K Q^T for the pair's two tiles
+    f32x4 S[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m2 = 0; m2 < 4; m2++) {
+        const u32x4 kk = *(const u32x4*)(kw + kaddr(16 * t + n, b * 4 + m2));
+        S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[0], kk[1]), qop[2 * m2], S[t], 0, 0, 0);
+        S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[2], kk[3]), qop[2 * m2 + 1], S[t], 0, 0, 0);
+      }
+    }
+    // ---- online softmax (column (a, j) = n: 4 lanes x 4 keys per tile)
+    float rmx = -1e30f;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        S[t][i] *= ksc;
+        rmx = __builtin_fmaxf(rmx, S[t][i]);
+      }
+    rmx = __builtin_fmaxf(rmx, __shfl_xor(rmx, 16));
+    rmx = __builtin_fmaxf(rmx, __shfl_xor(rmx, 32));
+    const float mnew = __builtin_fmaxf(mx, rmx);
+    const float corr = __builtin_amdgcn_exp2f(mx - mnew);  // rescales earlier rounds
+    mx = mnew;
+    f16x8 P;
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const _Float16 ph = (_Float16)__builtin_amdgcn_exp2f(S[t][i] - mnew);
+        P[t * 4 + i] = ph;
+        rs += (float)ph;
+      }
+    rs += __shfl_xor(rs, 16);
+    rs += __shfl_xor(rs, 32);
+    lsum = __builtin_fmaf(lsum, corr, rs);
+    // this lane's O rows are (kv head b, query head i); the correction of
+    // column (b, i) lives in lane 4b + i
+    float oc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) oc[i] = __shfl(corr, 4 * b + i);
+    // ---- O = O * corr + sv * (P V)
+    const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    const int kk8 = n >> 1, hb = n & 1;
+    const int key = kk8 < 4 ? 4 * b + kk8 : 16 + 4 * b + (kk8 - 4);
+    f32x4 T[4];
+#pragma unroll
+    for (int nu = 0; nu < 4; nu++) T[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mu = 0; mu < 4; mu++) {
+      const int sg = (b + mu) & 3;
+      const f16x8 A = ((n >> 2) == sg) ? P : zero8;
+#pragma unroll
+      for (int nu = 0; nu < 4; nu++) {
+        const u32x2 raw = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                       (lds_i32x2*)(vw + vaddr(key, sg * 4 + nu) + 8 * hb)));
+        T[nu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw[0], raw[1]), T[nu], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int nu = 0; nu < 4; nu++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) O[nu][i] = __builtin_fmaf(vsc, T[nu][i], O[nu][i] * oc[i]);
+  }
+  // ---- merge the waves (rows r = 4a + j); the K tiles hold the O rows now
+  __syncthreads();
+  typedef float MergeRows[16][D + 1];
+  MergeRows* sO = (MergeRows*)&klds[0][0];
+  if (l < 16) {
+    sm[w][l] = mx;
+    sl[w][l] = lsum;
+  }
+#pragma unroll
+  for (int nu = 0; nu < 4; nu++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) sO[w][4 * b + i][16 * nu + n] = O[nu][i];
+  __syncthreads();
+  const int r = tid >> 5, d0 = (tid & 31) * 2;
+  float M = sm[0][r];
+#pragma unroll
+  for (int v = 1; v < kDecWaves; v++) M = __builtin_fmaxf(M, sm[v][r]);
+  float L = 0.f, acc[2] = {0.f, 0.f};
+#pragma unroll
+  for (int v = 0; v < kDecWaves; v++) {
+    const float al = __builtin_amdgcn_exp2f(sm[v][r] - M);
+    L = __builtin_fmaf(sl[v][r], al, L);
+#pragma unroll
+    for (int e = 0; e < 2; e++) acc[e] = __builtin_fmaf(sO[v][r][d0 + e], al, acc[e]);
+  }
+  float* p = a.part + ((size_t)(half * 16 + r) * a.nwg + blockIdx.x) * kPart;
+  *(f32x2*)(p + 4 + d0) = f32x2{acc[0], acc[1]};
+  if ((tid & 31) == 0) {
+    p[0] = M;
+    p[1] = L;
+  }
+}
+
+// ---------------------------------------------------------------- finish
+// grid = 256 items (query head h = item >> 3, dims 8c..8c+7 with c = item & 7),
+// block = 64 (one wave).  Lane s holds FP8 partials s and s + 64; lane t
+// attends tail key committed + t.
+__global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
+  const int item = blockIdx.x, h = item >> 3, c = item & 7, kvh = h / GQA;
+  const int l = threadIdx.x;
+  const int ntail = a.qpos + 1 - a.committed;  // 0..64
+  // ---- every load first: partials, then the tail row of this lane
+  const float* ph = a.part + (size_t)h * a.nwg * kPart;
+  float pm[2], pl[2];
+  f32x4 po[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int s = l + 64 * u;
+    if (s < a.nwg) {
+      const float* pp = ph + (size_t)s * kPart;
+      pm[u] = pp[0];
+      pl[u] = pp[1];
+      po[u][0] = *(const f32x4*)(pp + 4 + 8 * c);
+      po[u][1] = *(const f32x4*)(pp + 8 + 8 * c);
+    } else {
+      pm[u] = -1e30f;
+      pl[u] = 0.f;
+      po[u][0] = po[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  u32x4 kq[8], qq[8], vv = u32x4{0u, 0u, 0u, 0u};
+  const bool live = l < ntail;
+  if (live) {
+    const bool fresh = a.knew && l == ntail - 1;
+    const uint16_t* kp = fresh ? a.knew + kvh * D : a.ktail + ((size_t)l * NKV + kvh) * D;
+    const uint16_t* vp = (fresh ? a.vnew + kvh * D : a.vtail + ((size_t)l * NKV + kvh) * D) + 8 * c;
+    const uint16_t* qp = a.q + (size_t)h * D;
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) {
+      kq[cc] = *(const u32x4*)(kp + 8 * cc);
+      qq[cc] = *(const u32x4*)(qp + 8 * cc);
+    }
+    vv = *(const u32x4*)vp;
+  }
+  // the fresh token joins the tail, written once per kv head
+  if (a.knew && c == 0 && h % GQA == 0 && l < 16) {
+    const int row = ntail - 1, cc = l & 7;
+    uint16_t* dst = (l < 8 ? a.ktail : a.vtail) + ((size_t)row * NKV + kvh) * D + cc * 8;
+    const uint16_t* src = (l < 8 ? a.knew : a.vnew) + kvh * D + cc * 8;
+    *(u32x4*)dst = *(const u32x4*)src;
+  }
+  // ---- tail scores (log2 units)
+  float x = -1e30f;
+  if (live) {
+    float sacc = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sacc = __builtin_fmaf(h2f((uint16_t)qq[cc][i]), h2f((uint16_t)kq[cc][i]), sacc);
+        sacc = __builtin_fmaf(h2f((uint16_t)(qq[cc][i] >> 16)), h2f((uint16_t)(kq[cc][i] >> 16)), sacc);
+      }
+    x = sacc * (a.scale * kLog2e);
+  }
+  // ---- one softmax over tail keys and partials
+  const float M = wave_max(__builtin_fmaxf(x, __builtin_fmaxf(pm[0], pm[1])));
+  const float pt = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
+  float L = pt, o[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    o[2 * i] = pt * h2f((uint16_t)vv[i]);
+    o[2 * i + 1] = pt * h2f((uint16_t)(vv[i] >> 16));
+  }
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const float wgt = pl[u] > 0.f ? __builtin_amdgcn_exp2f(pm[u] - M) : 0.f;
+    L = __builtin_fmaf(pl[u], wgt, L);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      o[e] = __builtin_fmaf(po[u][0][e], wgt, o[e]);
+      o[4 + e] = __builtin_fmaf(po[u][1][e], wgt, o[4 + e]);
+    }
+  }
+  L = wave_sum(L);
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = wave_sum(o[e]);
+  if (l == 0) {
+    const float inv = 1.f / L;
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      r[e] = (uint32_t)f2h(o[2 * e] * inv) | ((uint32_t)f2h(o[2 * e + 1] * inv) << 16);
+    *(u32x4*)(a.out + h * D + 8 * c) = r;
+  }
+}
+
+}  // namespace cia
+
+using namespace cia;
+
+// workgroups per half: about one pair per wave, at most one workgroup per CU
+// pair
+static int dec_nwg(int npairs) {
+  static int cap = 0;
+  if (cap == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus >= 2)
+      cap = cus / 2 < kMaxWgPerHalf ? cus / 2 : kMaxWgPerHalf;
+    else
+      cap = kMaxWgPerHalf;
+  }
+  int nwg = (npairs + kDecWaves - 1) / kDecWaves;
+  if (nwg < 1) nwg = 1;
+  return nwg > cap ? cap : nwg;
+}
+
+extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
+  if (max_tokens < 0) return 0;
+  return (int64_t)NH * kMaxWgPerHalf * kPart * (int64_t)sizeof(float);
+}
+
+// Flash-decoding with the library's split and, when knew/vnew are given, the
+// tail write of the fresh token fused in.  Internal entry shared by
+// cia_attn_decode and the layer driver.
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
+    const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
+    int64_t ws_bytes, void* stream) {
+  const int npairs = committed / 32;
+  const int nwg = dec_nwg(npairs);
+  if ((int64_t)NH * nwg * kPart * (int64_t)sizeof(float) > ws_bytes) return CIA_ERR_ARG;
+  DecodeArgs da{q, kc8, vc8, ksc, vsc, ktail, vtail, knew, vnew, committed, qpos, scale,
+                (float*)ws, npairs, nwg, out};
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_decode_attend, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
+  int st = launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(k_decode_finish, dim3(kItems), dim3(64), 0, s, da);
+  return launch_status();
+}

@@ -10,6 +10,12 @@
 
 #include "cuda_inf_attn.h"
 
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
+    const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
+    int64_t ws_bytes, void* stream);
+
 namespace cia {
 
 static thread_local int g_last_hip = 0;
@@ -225,10 +231,20 @@ int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int pa
       return cia_attn_decode_combine(L->pm, L->pl, L->po, out, L->nsplit, stream);
     }
     return cia_attn_decode(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
-                           past, scale, out, L->ws_decode, stream);
+                           past, scale, out, L->ws_decode, cia_decode_workspace_bytes(L->maxT),
+                           stream);
   }
   return cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
                              out, nullptr, S, past, scale, nullptr, stream);
+}
+
+// Single-token decode whose fresh token does not fill its group: the tail
+// write rides in the attention launch (no separate kv_write_tail launch).
+int decode_fused_append(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        uint16_t* out, int past, float scale, void* stream) {
+  return cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, k, v,
+                         L->committed, past, scale, out, L->ws_decode,
+                         cia_decode_workspace_bytes(L->maxT), stream);
 }
 
 }  // namespace
@@ -240,6 +256,9 @@ extern "C" int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t
   if (S < 1 || past < 0) return CIA_ERR_ARG;
   if (evicted) *evicted = -1;
   if (L->budget > 0) return h2o_forward(L, q, k, v, out, S, past, scale, evicted, stream);
+  if (S == 1 && L->nsplit == 0 && past - L->committed < CIA_KVGROUP - 1 &&
+      past >= L->committed && past < L->maxT)
+    return decode_fused_append(L, q, k, v, out, past, scale, stream);
   int st = group64_append(L, k, v, S, past, stream);
   if (st) return st;
   return group64_attend(L, q, out, S, past, scale, stream);
@@ -266,10 +285,18 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
     for (int l = 0; l < n_layers; l++) {
       const size_t r = (size_t)i * n_layers + l;
       cia_layer* L = &layers[l];
-      int st = group64_append(L, k + r * krow, v + r * krow, 1, past + i, stream);
-      if (st) return st;
+      const int pos = past + i;
+      int st;
+      const bool fused = L->nsplit == 0 && pos >= L->committed &&
+                         pos - L->committed < CIA_KVGROUP - 1 && pos < L->maxT;
+      if (!fused) {
+        st = group64_append(L, k + r * krow, v + r * krow, 1, pos, stream);
+        if (st) return st;
+      }
       if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r], s)))) return st;
-      st = group64_attend(L, q + r * qrow, out + r * qrow, 1, past + i, scale, stream);
+      st = fused ? decode_fused_append(L, q + r * qrow, k + r * krow, v + r * krow,
+                                       out + r * qrow, pos, scale, stream)
+                 : group64_attend(L, q + r * qrow, out + r * qrow, 1, pos, scale, stream);
       if (st) return st;
       if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r + 1], s)))) return st;
     }

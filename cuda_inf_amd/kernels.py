@@ -98,24 +98,26 @@ def attn_decode_combine(pm, pl, po, out, nsplit: int = NSPLIT_DEFAULT) -> None:
          nsplit, _stream())
 
 
-def decode_workspace_bytes() -> int:
-    return int(_lib.lib().cia_decode_workspace_bytes())
+def decode_workspace_bytes(max_tokens: int) -> int:
+    """Scratch bytes of attn_decode for contexts of up to max_tokens keys."""
+    return int(_lib.lib().cia_decode_workspace_bytes(max_tokens))
 
 
-def new_decode_workspace(device="cuda") -> torch.Tensor:
-    """Zero-filled workspace of the one-launch decode (its counters start at 0)."""
-    return torch.zeros(decode_workspace_bytes(), dtype=torch.uint8, device=device)
+def new_decode_workspace(max_tokens: int, device="cuda") -> torch.Tensor:
+    """Scratch of attn_decode (partial softmax states; no state between calls)."""
+    return torch.zeros(decode_workspace_bytes(max_tokens), dtype=torch.uint8, device=device)
 
 
 def attn_decode(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int, scale: float,
                 out, ws) -> None:
-    """Flash-decoding in one launch (replaces engine.cu:848-852's two launches)."""
+    """Flash-decoding on the matrix cores with the library's own split
+    (replaces engine.cu:848-852's split + combine launches)."""
     call("cia_attn_decode", _dev(q, "q", _F16, NH * D),
          _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
          _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
          _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
          committed, qpos, float(scale), _dev(out, "out", _F16, NH * D),
-         _dev(ws, "ws", (torch.uint8,), decode_workspace_bytes()), _stream())
+         _dev(ws, "ws", (torch.uint8,), decode_workspace_bytes(qpos + 1)), ws.numel(), _stream())
 
 
 # ------------------------------------------------------------ H2O

@@ -58,8 +58,9 @@ def h2o_pick_slots(n_live: int, C: int, W: int, slotpos: np.ndarray, attn_host: 
 class AttnLayer:
     """Device buffers of one attention layer (engine.cu:596-613, 731-770).
 
-    ``nsplit`` > 0 runs the reference's two-launch flash-decoding with that
-    split count; ``nsplit`` = 0 runs the one-launch decode.  ``budget`` > 0
+    ``nsplit`` > 0 runs the reference's flash-decoding split + combine with
+    that split count; ``nsplit`` = 0 runs the matrix-core decode with the
+    library's own split (and the tail write fused into it).  ``budget`` > 0
     enables H2O eviction with a ``budget``-slot buffer and local ``window``
     (0 -> budget/2, clamped as the reference does against ``prompt_len``).
     """
@@ -83,7 +84,7 @@ class AttnLayer:
         self.pm = torch.zeros(NH * ns, dtype=f32, device=dev)
         self.pl = torch.zeros(NH * ns, dtype=f32, device=dev)
         self.po = torch.zeros(NH * ns * D, dtype=f32, device=dev)
-        self.ws_decode = torch.zeros(decode_workspace_bytes(), dtype=u8, device=dev)
+        self.ws_decode = torch.zeros(decode_workspace_bytes(max_tokens), dtype=u8, device=dev)
         s = cia_layer()
         for name in ("kc8", "vc8", "ksc", "vsc", "ktail", "vtail", "pm", "pl", "po", "ws_decode"):
             setattr(s, name, getattr(self, name).data_ptr())

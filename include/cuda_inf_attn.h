@@ -131,18 +131,20 @@ int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
 int cia_attn_decode_combine(const float* pm, const float* pl, const float* po,
                             uint16_t* out, int nsplit, void* stream);
 
-/* Flash-decoding in one launch (no counterpart kernel in the reference; it
- * replaces the pair of launches at engine.cu:848-852).  Same result as
- * cia_attn_decode_split followed by cia_attn_decode_combine with the
- * workspace's own split count.  ws: cia_decode_workspace_bytes() bytes of
- * device memory, zero-filled once before first use (the kernel leaves its
- * counters at zero again after every call). */
+/* Flash-decoding with the library's own split on the matrix cores (no
+ * counterpart kernel in the reference; it replaces the pair of launches at
+ * engine.cu:848-852 and computes the same attention).  One workgroup per
+ * four 64-key FP8 groups of four kv heads, plus tail workgroups, then one
+ * merge launch.  Requires committed <= qpos + 1 (the tail holds keys
+ * committed..qpos).  ws: device scratch of at least
+ * cia_decode_workspace_bytes(qpos + 1) bytes, passed with its size. */
 int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                     const uint16_t* ksc, const uint16_t* vsc,
                     const uint16_t* ktail, const uint16_t* vtail,
                     int committed, int qpos, float scale, uint16_t* out,
-                    void* ws, void* stream);
-int64_t cia_decode_workspace_bytes(void);
+                    void* ws, int64_t ws_bytes, void* stream);
+/* scratch bytes cia_attn_decode needs for contexts of up to max_tokens */
+int64_t cia_decode_workspace_bytes(int max_tokens);
 
 /* ------------------------------------------------------------------ */
 /* H2O eviction                                                       */
@@ -222,9 +224,9 @@ typedef struct cia_layer {
   int maxT;
   int committed;
   /* flash-decoding */
-  int nsplit;            /* 0 -> fused one-launch decode with ws_decode */
+  int nsplit;            /* 0 -> cia_attn_decode path with ws_decode */
   float* pm; float* pl; float* po;
-  void* ws_decode;       /* cia_decode_workspace_bytes() */
+  void* ws_decode;       /* cia_decode_workspace_bytes(maxT) bytes */
   /* H2O (budget > 0 enables it) */
   int budget, window;
   uint8_t* kf; uint8_t* vf; uint16_t* ks; uint16_t* vs;

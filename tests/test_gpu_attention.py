@@ -1,7 +1,7 @@
 """GPU parity of the attention kernels against the oracle (tolerance
 2e-3 abs + 1e-3 rel of the fp32 oracle output).
 
-Flash-decoding split/combine (engine.cu:396-480), the one-launch decode, and
+Flash-decoding split/combine (engine.cu:396-480), the matrix-core decode, and
 attention_fused (engine.cu:236-308) on the group-64 FP8 cache.
 """
 import numpy as np
@@ -92,20 +92,19 @@ def test_decode_nsplit_sweep(orc, cia, dev, nsplit):
     assert np.all(pm.cpu().numpy()[empty] == np.float32(-1e30))
 
 
-@pytest.mark.parametrize("ntok", [1, 63, 64, 65, 2032, 5000])
-def test_decode_one_launch(orc, cia, dev, ntok):
+@pytest.mark.parametrize("ntok", [1, 63, 64, 65, 127, 128, 129, 255, 256, 257, 2032, 5000, 33000])
+def test_decode_matrix_cores(orc, cia, dev, ntok):
     from cuda_inf_amd import kernels as K
     L, ref, _ = _build(dev, orc, ntok, seed=ntok, outliers=True)
-    ws = K.new_decode_workspace(dev)
+    ws = K.new_decode_workspace(ntok, dev)
     q = _decode_q(ntok + 1, ntok - 1)
     _, r32, _ = orc.attn_decode(_u16(q), ref, ntok - 1, nsplit=16, nthreads=8)
-    for rep in range(3):  # the counters re-arm themselves
+    for rep in range(3):  # repeated calls reuse the workspace
         out = torch.empty((32, 64), dtype=torch.float16, device=dev)
         K.attn_decode(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed,
                       ntok - 1, 0.125, out, ws)
         torch.cuda.synchronize()
         assert_close_f16(_u16(out), r32, what=f"rep {rep}")
-    assert int(ws[:32].view(torch.int32).abs().sum()) == 0
 
 
 @pytest.mark.parametrize("S,past", [(1, 0), (333, 0), (64, 0), (50, 100), (130, 64), (700, 0)])
@@ -136,7 +135,7 @@ def test_decode_steps_through_commit(orc, cia, dev):
     from cuda_inf_amd.layer import AttnLayer
     from cuda_inf_amd.workload import qkv
     n0 = 4000
-    L = AttnLayer(n0 + 200, nsplit=0, device=dev)  # one-launch decode
+    L = AttnLayer(n0 + 200, nsplit=0, device=dev)  # matrix-core decode, fused tail write
     ref = orc.Group64Cache(n0 + 200)
     q0, k0, v0 = qkv(n0, seed=11, device="cpu", outliers=True)
     L.forward(q0.to(dev), k0.to(dev), v0.to(dev), 0)
