@@ -35,6 +35,13 @@ def algo_bytes(Tc: int, Tt: int) -> int:
     return 1024 * Tc + (Tc // 64) * 8 * 2 * 2 + 2048 * Tt + 8192
 
 
+def attend_bytes(Tc: int) -> int:
+    """Algorithmic bytes of the attend launch alone: the committed FP8 K+V,
+    their fp16 group scales and q (the tail and the output belong to the
+    finish launch)."""
+    return 1024 * Tc + (Tc // 64) * 8 * 2 * 2 + 4096
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -49,6 +56,13 @@ def main():
     ap.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", type=float, default=None,
+                    help="HBM bytes per attend launch measured with rocprofv3 --pmc "
+                         "(FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), reported as "
+                         "roofline.traffic")
+    ap.add_argument("--calib-copy", type=int, default=0,
+                    help="MiB: first run a plain device copy of this size three times "
+                         "(the reference dispatch that scales rocprofv3 byte counters)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         sys.exit("bench.py measures one GPU: the attention path runs on a single MI355X; "
@@ -67,6 +81,16 @@ def main():
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
+
+    if a.calib_copy > 0:
+        n = a.calib_copy << 18
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 3 x {a.calib_copy} MiB read + written")
+        del src, dst
 
     # ---- caches: ctx tokens per layer, loaded through the append loop
     layers = []
@@ -126,8 +150,18 @@ def main():
     timed_bytes = bytes_of_steps(s_timed, K)
     log(f"warm: {us_tok:.2f} us/token, effective {timed_bytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s")
 
-    # ---- per-kernel timing: events around each layer's attention launch
-    nev = 2 * K * nL
+    # The decode launch pair (k_decode_attend + k_decode_finish) is the
+    # dominant work: its average duration is the timed region's span over
+    # its K * layers launches (events bracket the region on the kernels' own
+    # stream; 1 step in 64 also carries that layer's tail write + commit).
+    pair_us = warm_ms * 1e3 / (K * nL)
+    pair_bytes = timed_bytes / (K * nL)
+    achieved = pair_bytes / (pair_us * 1e-6) / 1e9
+
+    # ---- attribution within the pair: HIP events recorded by the decode loop
+    # before, between and after each layer's two launches (each event adds
+    # its own marker overhead, so these sum to more than pair_us)
+    nev = 3 * K * nL
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(nev)]
     for e in evs:  # the hipEvent_t handles exist once recorded
         e.record(stream)
@@ -136,12 +170,13 @@ def main():
     s_k = cur["step"]
     run(K, ev_arr)
     torch.cuda.synchronize()
-    durs = [evs[2 * r].elapsed_time(evs[2 * r + 1]) for r in range(K * nL)]
-    kern_ms = sum(durs) / len(durs)
-    kern_bytes = bytes_of_steps(s_k, K) / (K * nL)
-    achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
-    log(f"decode kernel: {kern_ms * 1e3:.2f} us avg, {kern_bytes / 1e6:.2f} MB/launch, "
-        f"{achieved:.0f} GB/s")
+    att = [evs[3 * r].elapsed_time(evs[3 * r + 1]) for r in range(K * nL)]
+    fin = [evs[3 * r + 1].elapsed_time(evs[3 * r + 2]) for r in range(K * nL)]
+    att_us, fin_us = sum(att) / len(att) * 1e3, sum(fin) / len(fin) * 1e3
+    att_bytes = sum(attend_bytes(((ctx + i + 1) // 64) * 64) for i in range(s_k, s_k + K)) / K
+    log(f"decode pair: {pair_us:.2f} us per layer, {pair_bytes / 1e6:.2f} MB, {achieved:.0f} GB/s; "
+        f"event-bracketed: attend {att_us:.2f} us ({att_bytes / (att_us * 1e-6) / 1e9:.0f} GB/s), "
+        f"finish {fin_us:.2f} us")
 
     # ---- cold: evict the KV from the 256 MB Infinity Cache before every token
     # by reading 1 GiB of other data (a read leaves no dirty lines behind)
@@ -195,6 +230,7 @@ def main():
         cpu = cpu_baseline(layers[0], arr[0].committed, ctx + cur["step"] - 1, q, nL,
                            a.cpu_seconds, log)
 
+    traffic = a.traffic if a.traffic is not None else measured_traffic(ctx, nL)
     res = {
         "metric": "decode-attn µs/token + HBM GB/s (% of 8 TB/s) at 32k ctx; prefill MFMA util",
         "value": round(us_tok, 3),
@@ -216,13 +252,33 @@ def main():
         "cold_us_per_token": round(cold_us, 3) if cold_us else None,
         "effective_gbps_cold": round(mean_tok_bytes / (cold_us * 1e-6) / 1e9, 1) if cold_us else None,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_decode_attend + k_decode_finish", "algo_bytes_per_launch": int(kern_bytes),
-                     "avg_launch_us": round(kern_ms * 1e3, 3)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": "decode launch pair k_decode_attend + k_decode_finish",
+                     "algo_bytes_per_launch": int(pair_bytes),
+                     "avg_launch_us": round(pair_us, 3),
+                     "event_bracketed_us": {"k_decode_attend": round(att_us, 3),
+                                            "k_decode_finish": round(fin_us, 3)}},
         "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+
+def measured_traffic(ctx: int, nL: int):
+    """HBM bytes per decode launch pair from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) when it was taken on
+    this workload; None otherwise."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                     "decode_pair_ctx32k_traffic.json")
+    try:
+        with open(p) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("context") != ctx or t.get("layers") != nL:
+        return None
+    return t.get("pair_bytes_per_launch")
 
 
 def cpu_baseline(L, committed, qpos, q, nL, seconds, log):

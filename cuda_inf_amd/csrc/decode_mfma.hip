@@ -111,27 +111,34 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   for (int v = 0; v < 4; v++) O[v] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p = p0; p < p1; p++) {
     const int kbase = p * 32;
-    // ---- loads: instruction i covers keys 4i..4i+3, lane -> (key 4i + b, chunk n)
+    // ---- loads: instruction i covers keys 4i..4i+3, lane -> (key 4i + b, chunk n);
+    // all K first, so S^T and the softmax run while V is still arriving
+    // (the group scales are loaded first: waiting for them then waits for
+    // nothing else)
+    const int grp = kbase >> 6;
+    const uint16_t ksc_h = a.ksc[grp * NKV + half * 4 + (n >> 2)];
+    const uint16_t vsc_h = a.vsc[grp * NKV + half * 4 + b];
     u32x4 kr[8], vr[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const size_t off = (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16;
-      kr[i] = *(const u32x4*)(a.kc8 + off);
-      vr[i] = *(const u32x4*)(a.vc8 + off);
-    }
+    for (int i = 0; i < 8; i++)
+      kr[i] = *(const u32x4*)(a.kc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      vr[i] = *(const u32x4*)(a.vc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
     // K scale of this lane's column kv head (times scale*log2e), V scale of
     // this lane's row kv head
-    const int grp = kbase >> 6;
-    const float ksc = h2f(a.ksc[grp * NKV + half * 4 + (n >> 2)]) * qscale;
-    const float vsc = h2f(a.vsc[grp * NKV + half * 4 + b]);
-#pragma unroll
-    for (int i = 0; i < 8; i++) *(u32x4*)(kw + kaddr(4 * i + b, n)) = kr[i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) *(u32x4*)(vw + vaddr(4 * i + b, n)) = vr[i];
-    // ---- S^T = K Q^T for the pair's two tiles
+    const float ksc = h2f(ksc_h) * qscale;
+    const float vsc = h2f(vsc_h);
+    // ---- S^T = K Q^T for the pair's two tiles; tile t (keys 16t..16t+15)
+    // needs only load instructions 4t..4t+3
     f32x4 S[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) {
+      // (the scheduling barriers keep later tiles' LDS stores, which wait
+      // for their loads, behind this tile's matrix products)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 4 * t; i < 4 * t + 4; i++) *(u32x4*)(kw + kaddr(4 * i + b, n)) = kr[i];
       S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m2 = 0; m2 < 4; m2++) {
@@ -173,6 +180,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; i++) oc[i] = __shfl(corr, 4 * b + i);
     // ---- O = O * corr + sv * (P V)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) *(u32x4*)(vw + vaddr(4 * i + b, n)) = vr[i];
     const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     const int kk8 = n >> 1, hb = n & 1;
     const int key = kk8 < 4 ? 4 * b + kk8 : 16 + 4 * b + (kk8 - 4);
@@ -230,11 +240,15 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
 }
 
 // ---------------------------------------------------------------- finish
-// grid = 256 items (query head h = item >> 3, dims 8c..8c+7 with c = item & 7),
-// block = 64 (one wave).  Lane s holds FP8 partials s and s + 64; lane t
-// attends tail key committed + t.
+// grid = 256 items (query head h, dims 8c..8c+7), block = 64 (one wave).
+// Workgroups are handed to the 8 XCDs round-robin (XCD = blockIdx.x mod 8),
+// so item b takes h = 4 (b mod 8) + (b div 64) and c = (b div 8) mod 8: the
+// 8 items of a head -- and the 4 heads of one kv head -- share an XCD and
+// read that head's partials and tail rows through one L2.  Lane s holds FP8
+// partials s and s + 64; lane t attends tail key committed + t.
 __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
-  const int item = blockIdx.x, h = item >> 3, c = item & 7, kvh = h / GQA;
+  const int j = blockIdx.x >> 3;
+  const int h = (blockIdx.x & 7) * 4 + (j >> 3), c = j & 7, kvh = h / GQA;
   const int l = threadIdx.x;
   const int ntail = a.qpos + 1 - a.committed;  // 0..64
   // ---- every load first: partials, then the tail row of this lane
@@ -351,12 +365,13 @@ extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
 
 // Flash-decoding with the library's split and, when knew/vnew are given, the
 // tail write of the fresh token fused in.  Internal entry shared by
-// cia_attn_decode and the layer driver.
+// cia_attn_decode and the layer driver; mid_event (may be NULL) is recorded
+// between the two launches, for per-kernel timing.
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
-    int64_t ws_bytes, void* stream) {
+    int64_t ws_bytes, void* stream, void* mid_event) {
   const int npairs = committed / 32;
   const int nwg = dec_nwg(npairs);
   if ((int64_t)NH * nwg * kPart * (int64_t)sizeof(float) > ws_bytes) return CIA_ERR_ARG;
@@ -366,6 +381,13 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   hipLaunchKernelGGL(k_decode_attend, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
   int st = launch_status();
   if (st) return st;
+  if (mid_event) {
+    const hipError_t e = hipEventRecord((hipEvent_t)mid_event, s);
+    if (e != hipSuccess) {
+      set_hip_error(e);
+      return CIA_ERR_HIP;
+    }
+  }
   hipLaunchKernelGGL(k_decode_finish, dim3(kItems), dim3(64), 0, s, da);
   return launch_status();
 }

@@ -14,7 +14,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
-    int64_t ws_bytes, void* stream);
+    int64_t ws_bytes, void* stream, void* mid_event);
 
 namespace cia {
 
@@ -221,30 +221,37 @@ int group64_append(cia_layer* L, const uint16_t* k, const uint16_t* v, int S, in
 }
 
 int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int past, float scale,
-                   void* stream) {
+                   void* stream, void* mid_event = nullptr) {
   if (S == 1) {
     if (L->nsplit > 0) {
       int st = cia_attn_decode_split(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail,
                                      L->committed, past, scale, L->pm, L->pl, L->po, L->nsplit,
                                      stream);
       if (st) return st;
+      if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
+        return st;
       return cia_attn_decode_combine(L->pm, L->pl, L->po, out, L->nsplit, stream);
     }
-    return cia_attn_decode(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
-                           past, scale, out, L->ws_decode, cia_decode_workspace_bytes(L->maxT),
-                           stream);
+    if (L->committed > past + 1 || past - L->committed >= CIA_KVGROUP) return CIA_ERR_STATE;
+    return cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, nullptr,
+                           nullptr, L->committed, past, scale, out, L->ws_decode,
+                           cia_decode_workspace_bytes(L->maxT), stream, mid_event);
   }
-  return cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, L->committed,
-                             out, nullptr, S, past, scale, nullptr, stream);
+  int st = cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail,
+                               L->committed, out, nullptr, S, past, scale, nullptr, stream);
+  if (st) return st;
+  if (mid_event) return hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream));
+  return CIA_OK;
 }
 
 // Single-token decode whose fresh token does not fill its group: the tail
 // write rides in the attention launch (no separate kv_write_tail launch).
 int decode_fused_append(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                        uint16_t* out, int past, float scale, void* stream) {
+                        uint16_t* out, int past, float scale, void* stream,
+                        void* mid_event = nullptr) {
   return cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, k, v,
                          L->committed, past, scale, out, L->ws_decode,
-                         cia_decode_workspace_bytes(L->maxT), stream);
+                         cia_decode_workspace_bytes(L->maxT), stream, mid_event);
 }
 
 }  // namespace
@@ -293,12 +300,13 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
         st = group64_append(L, k + r * krow, v + r * krow, 1, pos, stream);
         if (st) return st;
       }
-      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r], s)))) return st;
+      void* mid = events ? events[3 * r + 1] : nullptr;
+      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r], s)))) return st;
       st = fused ? decode_fused_append(L, q + r * qrow, k + r * krow, v + r * krow,
-                                       out + r * qrow, pos, scale, stream)
-                 : group64_attend(L, q + r * qrow, out + r * qrow, 1, pos, scale, stream);
+                                       out + r * qrow, pos, scale, stream, mid)
+                 : group64_attend(L, q + r * qrow, out + r * qrow, 1, pos, scale, stream, mid);
       if (st) return st;
-      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[2 * r + 1], s)))) return st;
+      if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
     }
   }
   return CIA_OK;

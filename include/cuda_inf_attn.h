@@ -259,9 +259,12 @@ int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t* v,
  * attention branches: for step s in [0, steps) and layer l in [0, n_layers)
  * runs cia_layer_forward(&layers[l], q[s][l], k[s][l], v[s][l],
  * out[s][l], 1, past + s, ...).  q/out: fp16 [steps][n_layers][32][64],
- * k/v: fp16 [steps][n_layers][8][64].  events (may be NULL): 2*steps*n_layers
- * hipEvent_t recorded before and after each layer's attention launch(es)
- * (after the append), for per-kernel timing.  Group-64 layers only. */
+ * k/v: fp16 [steps][n_layers][8][64].  events (may be NULL): 3*steps*n_layers
+ * hipEvent_t; for (step s, layer l), r = s*n_layers + l, events[3r] is
+ * recorded before the layer's attention launches (after any separate append
+ * launches), events[3r+1] between the first attention launch and the second
+ * (after the only one when there is one) and events[3r+2] after the last:
+ * per-kernel timing on the stream the kernels run on.  Group-64 layers only. */
 int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
                     const uint16_t* k, const uint16_t* v, uint16_t* out,
                     int past, int steps, float scale, void** events,
