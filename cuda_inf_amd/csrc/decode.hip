@@ -1,5 +1,7 @@
 // decode.hip -- flash-decoding over the group-64 FP8 cache on gfx950
-// (engine.cu:386-480) and the fused causal prefill (engine.cu:236-308).
+// (engine.cu:386-480) and the entry points of the fused causal prefill
+// (engine.cu:236-308, kernel in prefill_mfma.hip) and of the matrix-core
+// decode (decode_mfma.hip).
 //
 // The reference launches one block per (query head, split) and so reads
 // every K/V byte four times (once per query head of a GQA group).  Here a
@@ -61,21 +63,6 @@ __global__ __launch_bounds__(64) void k_decode_combine(const float* __restrict__
                                                        uint16_t* __restrict__ out, int nsplit) {
   const int h = blockIdx.x, d = threadIdx.x;
   out[h * D + d] = f2h(combine_one(pm, pl, po, h, d, nsplit));
-}
-
-// ---------------------------------------------------------------- prefill
-// attention_fused: grid = (S, 8 kv heads), block = 256; query i attends keys
-// [0, past+i] (FP8 below `committed`, tail above).
-__global__ __launch_bounds__(256) void k_prefill(const uint16_t* __restrict__ q, Group64Cache c,
-                                                 uint16_t* __restrict__ out, int past,
-                                                 float scale) {
-  __shared__ float lds[kRangeLds];
-  __shared__ float sM[4], sL[4], sO[4 * D];
-  const int i = blockIdx.x, kvh = blockIdx.y;
-  const uint16_t* qi = q + (size_t)i * NH * D;
-  attend_range(qi, c, kvh, scale, 0, past + i + 1, lds, sM, sL, sO);
-  const int j = threadIdx.x >> 6, d = threadIdx.x & 63;
-  out[((size_t)i * NH + kvh * GQA + j) * D + d] = f2h(sO[j * D + d] * (1.f / sL[j]));
 }
 
 }  // namespace cia
@@ -143,6 +130,11 @@ extern "C" __attribute__((visibility("hidden"))) int cia_mass_group64(const uint
                                 const uint16_t* ktail, int committed, float* attn_sum, int S,
                                 int past, float scale, void* ws, void* stream);
 
+extern "C" __attribute__((visibility("hidden"))) int cia_prefill_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed,
+    uint16_t* out, int S, int past, float scale, void* stream);
+
 extern "C" int cia_attention_fused(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                                    const uint16_t* ksc, const uint16_t* vsc,
                                    const uint16_t* ktail, const uint16_t* vtail, int committed,
@@ -155,10 +147,9 @@ extern "C" int cia_attention_fused(const uint16_t* q, const uint8_t* kc8, const 
   CIA_REQUIRE(out, CIA_ERR_NULL);
   CIA_REQUIRE(aligned(out, 2), CIA_ERR_ALIGN);
   CIA_REQUIRE(past + S - 1 - committed < G, CIA_ERR_STATE);
-  Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
-  hipLaunchKernelGGL(k_prefill, dim3(S, NKV), dim3(256), 0, (hipStream_t)stream, q, c, out, past,
-                     scale);
-  st = launch_status();
+  CIA_REQUIRE(scale >= 0.0f && scale < __builtin_inff(), CIA_ERR_ARG);
+  st = cia_prefill_mfma(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, out, S, past, scale,
+                        stream);
   if (st || !attn_sum) return st;
   return cia_mass_group64(q, kc8, ksc, ktail, committed, attn_sum, S, past, scale, ws, stream);
 }

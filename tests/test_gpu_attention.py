@@ -130,6 +130,44 @@ def test_attention_fused(orc, cia, dev, S, past):
     assert_close_f16(_u16(out), r32)
 
 
+@pytest.mark.parametrize("S,past,outliers,zero_group", [
+    (2, 0, False, False), (63, 0, False, False), (65, 0, True, False), (128, 0, False, True),
+    (200, 1000, True, False), (17, 4079, False, False), (1000, 37, True, True),
+    (4096, 0, True, False)])
+def test_prefill_matrix_cores(orc, cia, dev, S, past, outliers, zero_group):
+    """The matrix-core causal prefill (attention_fused): blocks of 64 queries,
+    heavy/light block pairs, FP8 groups plus the fp16 tail, lazily moved
+    running max; a K/V group of zeros has scale 0.  Large S is checked on a
+    subset of query rows."""
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    L = AttnLayer(past + S + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(past + S + 64)
+    if past:
+        q0, k0, v0 = qkv(past, seed=11, device="cpu", outliers=outliers)
+        if zero_group and past >= 128:
+            k0[64:128] = 0
+            v0[64:128] = 0
+        L.forward(q0.to(dev), k0.to(dev), v0.to(dev), 0)
+        ref.append(_u16(k0), _u16(v0), 0)
+    q, k, v = qkv(S, seed=12, device="cpu", past=past, outliers=outliers)
+    if zero_group and not past:
+        k[64:128] = 0
+        v[64:128] = 0
+    out, _ = L.forward(q.to(dev), k.to(dev), v.to(dev), past)
+    ref.append(_u16(k), _u16(v), past)
+    torch.cuda.synchronize()
+    rows = None
+    if S > 1200:
+        rows = np.unique(np.concatenate([np.arange(0, 70), np.arange(S - 70, S),
+                                         np.arange(0, S, 37)])).astype(np.int32)
+    _, r32 = orc.attention_fused(_u16(q), ref, S, past, rows=rows)
+    got = _u16(out)
+    if rows is not None:
+        got, r32 = got[rows], r32[rows]
+    assert_close_f16(got, r32)
+
+
 def test_decode_steps_through_commit(orc, cia, dev):
     """Decode steps that cross a group boundary (tail fills, commit, new tail)."""
     from cuda_inf_amd.layer import AttnLayer
