@@ -79,72 +79,218 @@ __device__ __forceinline__ f16x8 pf_cvt8(uint32_t w0, uint32_t w1) {
 }
 
 // One thread's share of a tile in flight: K key tid >> 3, dims 8 (tid & 7)
-// .. +7; V keys 2 (tid & 31) and +1, dims 4 (tid >> 5) .. +3.
-struct PfStage {
-  u32x4 k;        // 8 fp8 bytes (k.x, k.y) or 8 fp16 values
-  u32x2 v0, v1;   // 4 fp8 bytes (v0.x) or 4 fp16 values, keys 2kp and 2kp+1
-  uint16_t vs;    // V scale (fp16 bits); 0x3C00 = 1 for the tail
-  bool fp8;
+// .. +7; V keys 2 (tid & 31) and +1, dims 4 (tid >> 5) .. +3.  FP8 tiles and
+// the fp16 tail use separate registers, so a prefetch never waits on the
+// previous one.
+struct PfStage8 {
+  u32x2 k;           // 8 fp8 K bytes
+  uint32_t v0, v1;   // 4 fp8 V bytes of keys 2kp, 2kp+1
+  uint16_t ks, vs;   // group scales (fp16 bits)
+};
+struct PfStage16 {
+  u32x4 k;           // 8 fp16 K values
+  u32x2 v0, v1;      // 4 fp16 V values of keys 2kp, 2kp+1
 };
 
-__device__ __forceinline__ void pf_load(const PrefillArgs& a, int g, int j, int nvalid, int tid,
-                                        PfStage& st) {
+__device__ __forceinline__ void pf_load8(const PrefillArgs& a, int g, int j, int tid,
+                                         PfStage8& st) {
   const int kkey = tid >> 3, kch = tid & 7, kp = tid & 31, dc = tid >> 5;
-  st.fp8 = (j << 6) < a.committed;
-  if (st.fp8) {
-    const size_t kb = (size_t)(64 * j + kkey) * NKV + g;
-    const u32x2 kk = *(const u32x2*)(a.kc8 + kb * D + 8 * kch);
-    st.k = u32x4{kk[0], kk[1], 0u, 0u};
-    const size_t v0 = (size_t)(64 * j + 2 * kp) * NKV + g;
-    st.v0 = u32x2{*(const uint32_t*)(a.vc8 + v0 * D + 4 * dc), 0u};
-    st.v1 = u32x2{*(const uint32_t*)(a.vc8 + (v0 + NKV) * D + 4 * dc), 0u};
-    st.vs = a.vsc[j * NKV + g];
-  } else {
-    // tail rows 0..nvalid-1 (keys committed..); others stage as zeros
-    const u32x4 z4 = u32x4{0u, 0u, 0u, 0u};
-    const u32x2 z2 = u32x2{0u, 0u};
-    st.k = kkey < nvalid ? *(const u32x4*)(a.ktail + ((size_t)kkey * NKV + g) * D + 8 * kch) : z4;
-    st.v0 = 2 * kp < nvalid
-                ? *(const u32x2*)(a.vtail + ((size_t)(2 * kp) * NKV + g) * D + 4 * dc) : z2;
-    st.v1 = 2 * kp + 1 < nvalid
-                ? *(const u32x2*)(a.vtail + ((size_t)(2 * kp + 1) * NKV + g) * D + 4 * dc) : z2;
-    st.vs = 0x3C00;
-  }
+  st.ks = a.ksc[j * NKV + g];
+  st.vs = a.vsc[j * NKV + g];
+  st.k = *(const u32x2*)(a.kc8 + ((size_t)(64 * j + kkey) * NKV + g) * D + 8 * kch);
+  const size_t v0 = (size_t)(64 * j + 2 * kp) * NKV + g;
+  st.v0 = *(const uint32_t*)(a.vc8 + v0 * D + 4 * dc);
+  st.v1 = *(const uint32_t*)(a.vc8 + (v0 + NKV) * D + 4 * dc);
 }
 
-__device__ __forceinline__ void pf_store(uint8_t* buf, int tid, const PfStage& st) {
+// tail rows 0..nvalid-1 (keys committed..); the others stage as zeros
+__device__ __forceinline__ void pf_load16(const PrefillArgs& a, int g, int nvalid, int tid,
+                                          PfStage16& st) {
   const int kkey = tid >> 3, kch = tid & 7, kp = tid & 31, dc = tid >> 5;
-  u32x4 kw = st.k;
-  f16x4 va, vb;
-  if (st.fp8) {
-    kw = __builtin_bit_cast(u32x4, pf_cvt8(st.k[0], st.k[1]));
-    const _Float16 s = __builtin_bit_cast(_Float16, st.vs);
-    const f16x2 s2 = f16x2{s, s};
-    const f16x2 a0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v0[0], 1.0f, false) * s2;
-    const f16x2 a1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v0[0], 1.0f, true) * s2;
-    const f16x2 b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1[0], 1.0f, false) * s2;
-    const f16x2 b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1[0], 1.0f, true) * s2;
-    va = f16x4{a0[0], a0[1], a1[0], a1[1]};
-    vb = f16x4{b0[0], b0[1], b1[0], b1[1]};
-  } else {
-    va = __builtin_bit_cast(f16x4, st.v0);
-    vb = __builtin_bit_cast(f16x4, st.v1);
-  }
+  st.k = u32x4{0u, 0u, 0u, 0u};
+  st.v0 = st.v1 = u32x2{0u, 0u};
+  if (kkey < nvalid) st.k = *(const u32x4*)(a.ktail + ((size_t)kkey * NKV + g) * D + 8 * kch);
+  if (2 * kp < nvalid) st.v0 = *(const u32x2*)(a.vtail + ((size_t)(2 * kp) * NKV + g) * D + 4 * dc);
+  if (2 * kp + 1 < nvalid)
+    st.v1 = *(const u32x2*)(a.vtail + ((size_t)(2 * kp + 1) * NKV + g) * D + 4 * dc);
+}
+
+// K row chunk and the V^T words of this thread; the upper half-wave writes
+// its dims in the order 1,0,3,2 (spreads the writes over all LDS banks)
+__device__ __forceinline__ void pf_store(uint8_t* buf, int tid, u32x4 kw, f16x4 va, f16x4 vb) {
+  const int kkey = tid >> 3, kch = tid & 7, kp = tid & 31, dc = tid >> 5;
   *(u32x4*)(buf + pf_kaddr(kkey, kch)) = kw;
-  // V^T: dims 4dc + e, the pair (key 2kp, key 2kp+1) as one 32-bit word;
-  // the upper half-wave writes its dims in the order 1,0,3,2 (bank spread)
   const int slot = pf_vslot(2 * kp);
   const int flip = (tid >> 5) & 1;
   uint8_t* vt = buf + kPfTileBytes;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
-    const int ee = e ^ flip;
     const _Float16 x0 = flip ? va[e ^ 1] : va[e];
     const _Float16 x1 = flip ? vb[e ^ 1] : vb[e];
     const uint32_t word = (uint32_t)__builtin_bit_cast(uint16_t, x0) |
                           ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-    *(uint32_t*)(vt + pf_vaddr(4 * dc + ee, slot)) = word;
+    *(uint32_t*)(vt + pf_vaddr(4 * dc + (e ^ flip), slot)) = word;
   }
+}
+
+// A group scale loaded two tiles ahead, read when its tile is staged.  The
+// empty asm makes the value opaque to the compiler's uniformity analysis, so
+// it is not moved into a scalar register (which would wait for the load the
+// moment it is issued).
+__device__ __forceinline__ uint32_t pf_late(uint16_t x) {
+  uint32_t v = x;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+// K scale -> score multiplier base (times scale * log2e later); scores of a
+// group whose K scale is 0 are 0, and the multiplier is kept >= 1e-30 where
+// it is used so that masked keys (-inf) stay -inf
+__device__ __forceinline__ float pf_scale(uint16_t ks) { return h2f((uint16_t)pf_late(ks)); }
+
+__device__ __forceinline__ void pf_store8(uint8_t* buf, int tid, const PfStage8& st) {
+  const u32x4 kw = __builtin_bit_cast(u32x4, pf_cvt8(st.k[0], st.k[1]));
+  const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)pf_late(st.vs));
+  const f16x2 s2 = f16x2{s, s};
+  const f16x2 a0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v0, 1.0f, false) * s2;
+  const f16x2 a1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v0, 1.0f, true) * s2;
+  const f16x2 b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1, 1.0f, false) * s2;
+  const f16x2 b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1, 1.0f, true) * s2;
+  pf_store(buf, tid, kw, f16x4{a0[0], a0[1], a1[0], a1[1]}, f16x4{b0[0], b0[1], b1[0], b1[1]});
+}
+
+__device__ __forceinline__ void pf_store16(uint8_t* buf, int tid, const PfStage16& st) {
+  pf_store(buf, tid, st.k, __builtin_bit_cast(f16x4, st.v0), __builtin_bit_cast(f16x4, st.v1));
+}
+
+// max over the 4 lanes {l, l^16, l^32, l^48} that hold one query column
+__device__ __forceinline__ float pf_colmax(float v) {
+  v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+  return __builtin_fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float pf_colsum(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+// Softmax numerators of one 16-query tile: S[kt] rows = keys 64j + 16kt +
+// 4b + i, column = query qpos.  P[u] is the B operand of key block u.
+// Returns the largest exponent used (log2 units above the running max).
+template <bool kMask>
+__device__ __forceinline__ float pf_exp(const f32x4 (&S)[4], float c, float m, int key0, int qpos,
+                                        f16x8 (&P)[2], float& rs) {
+  float tm = -__builtin_inff();
+  rs = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      t[i] = __builtin_fmaf(S[kt][i], c, -m);
+      if (kMask && key0 + 16 * kt + i > qpos) t[i] = -__builtin_inff();
+    }
+    tm = __builtin_fmaxf(tm, __builtin_fmaxf(__builtin_fmaxf(t[0], t[1]), __builtin_fmaxf(t[2], t[3])));
+#pragma unroll
+    for (int i = 0; i < 4; i++) P[kt >> 1][4 * (kt & 1) + i] = (_Float16)__builtin_amdgcn_exp2f(t[i]);
+  }
+  const f16x2 one = f16x2{(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      rs = __builtin_amdgcn_fdot2(f16x2{P[u][2 * e], P[u][2 * e + 1]}, one, rs, false);
+  return tm;
+}
+
+// Tile max above the running max beyond the headroom (rare after the first
+// tiles): move the running max to the column's tile max, rescale O and l,
+// recompute P.
+template <bool kMask>
+__device__ __forceinline__ void pf_remax(const f32x4 (&S)[4], float c, float& m, float& l,
+                                         f32x4 (&O)[4], int key0, int qpos, f16x8 (&P)[2],
+                                         float& rs) {
+  float cm = -__builtin_inff();
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const bool out = kMask && key0 + 16 * kt + i > qpos;
+      cm = __builtin_fmaxf(cm, out ? -__builtin_inff() : S[kt][i]);
+    }
+  cm = pf_colmax(cm);
+  const float mt = cm == -__builtin_inff() ? cm : cm * c;
+  if (mt > m + kPfLazy) {
+    const float corr = __builtin_amdgcn_exp2f(m - mt);  // 0 on the first tile
+    m = mt;
+    l *= corr;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) O[dt][i] *= corr;
+  }
+  pf_exp<kMask>(S, c, m, key0, qpos, P, rs);
+}
+
+// One 64-key tile for the wave's two 16-query tiles.  The second tile's
+// matrix products are issued before the first tile's exponentials, and the
+// first tile's P V before the second tile's exponentials, so the matrix
+// cores and the vector unit of one wave overlap.
+template <bool kMask>
+__device__ __forceinline__ void pf_tile(const uint8_t* kt_lds, const uint8_t* vt_lds,
+                                        const f16x8 (&qop)[2][2], float c, int key0, int qpos0,
+                                        int n, int b, f32x4 (&O)[4][2], float (&mrun)[2],
+                                        float (&lrun)[2]) {
+  f16x8 kop[4][2];
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+      kop[kt][kb] = *(const f16x8*)(kt_lds + pf_kaddr(16 * kt + n, 4 * kb + b));
+  f32x4 S0[4], S1[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++) {
+    S0[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kt][0], qop[0][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    S0[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kt][1], qop[0][1], S0[kt], 0, 0, 0);
+  }
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++) {
+    S1[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kt][0], qop[1][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    S1[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kt][1], qop[1][1], S1[kt], 0, 0, 0);
+  }
+  const int kb0 = key0 + 4 * b;
+  f16x8 P0[2], P1[2];
+  float rs0, rs1;
+  float tm = pf_exp<kMask>(S0, c, mrun[0], kb0, qpos0, P0, rs0);
+  if (__any(tm > kPfLazy)) {
+    f32x4 Oq[4] = {O[0][0], O[1][0], O[2][0], O[3][0]};
+    pf_remax<kMask>(S0, c, mrun[0], lrun[0], Oq, kb0, qpos0, P0, rs0);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) O[dt][0] = Oq[dt];
+  }
+  lrun[0] += rs0;
+  f16x8 vop[4][2];
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+      vop[dt][u] = *(const f16x8*)(vt_lds + pf_vaddr(16 * dt + n, 32 * u + 8 * b));
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+      O[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[dt][u], P0[u], O[dt][0], 0, 0, 0);
+  tm = pf_exp<kMask>(S1, c, mrun[1], kb0, qpos0 + 16, P1, rs1);
+  if (__any(tm > kPfLazy)) {
+    f32x4 Oq[4] = {O[0][1], O[1][1], O[2][1], O[3][1]};
+    pf_remax<kMask>(S1, c, mrun[1], lrun[1], Oq, kb0, qpos0 + 16, P1, rs1);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) O[dt][1] = Oq[dt];
+  }
+  lrun[1] += rs1;
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+      O[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[dt][u], P1[u], O[dt][1], 0, 0, 0);
 }
 
 // grid = 8 * ceil(nblk / 2), block = 512
@@ -154,6 +300,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
   const int g = blockIdx.x & 7, pr = blockIdx.x >> 3;
   const int h = g * GQA + (w & 3);
   const int nvalid_tail = a.past + a.S - a.committed;  // tail keys 0..63
+  const int nfp8 = a.committed >> 6;
 
   for (int phase = 0; phase < 2; phase++) {
     const int blk = phase == 0 ? a.nblk - 1 - pr : pr;
@@ -161,8 +308,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
     const int q0 = blk * kPfQ + 32 * (w >> 2);        // this wave's first query
     const int kend = a.past + min(a.S, (blk + 1) * kPfQ);  // keys 0..kend-1 for the block
     const int ntile = (kend + 63) >> 6;
-    const int qmin = a.past + q0;                                 // wave's first position
-    const int qlast = a.past + min(q0 + 31, a.S - 1);             // wave's last valid position
+    const int qmin = a.past + q0;                      // wave's first position
+    const int qlast = a.past + min(q0 + 31, a.S - 1);  // wave's last valid position
     const bool wave_live = q0 < a.S;
 
     // Q^T as the B operand: lane (n, b) holds query q0 + 16 qt + n, dims 32 kb + 8 b .. +7
@@ -182,114 +329,58 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
       for (int qt = 0; qt < 2; qt++) O[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrun[2] = {-__builtin_inff(), -__builtin_inff()}, lrun[2] = {0.f, 0.f};
 
-    PfStage st;
-    pf_load(a, g, 0, nvalid_tail, tid, st);
-    pf_store(lds[0], tid, st);
+    // Q must have arrived before the loop: an explicit vmcnt(0) here keeps
+    // the loop's waits for the K/V prefetch from covering it
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+
+    // FP8 tiles 0..nf-1 with a two-deep prefetch, then at most one fp16
+    // tail tile (the last one)
+    const int nf = min(ntile, nfp8);
+    const int qpos0 = a.past + q0 + n;
+    PfStage8 s8;
+    float c_cur = 1.0f, c_next = 1.0f;
+    if (nf > 0) {
+      pf_load8(a, g, 0, tid, s8);
+      c_cur = pf_scale(s8.ks);
+      pf_store8(lds[0], tid, s8);
+      if (nf > 1) pf_load8(a, g, 1, tid, s8);
+    }
     __syncthreads();
-    for (int j = 0; j < ntile; j++) {
-      if (j + 1 < ntile) pf_load(a, g, j + 1, nvalid_tail, tid, st);
-      const uint8_t* kt_lds = lds[j & 1];
-      const uint8_t* vt_lds = lds[j & 1] + kPfTileBytes;
+    for (int j = 0; j < nf; j++) {
+      // stage tile j+1 (loaded during tile j-1) into the free buffer, then
+      // start loading tile j+2
+      if (j + 1 < nf) {
+        c_next = pf_scale(s8.ks);
+        pf_store8(lds[(j + 1) & 1], tid, s8);
+        if (j + 2 < nf) pf_load8(a, g, j + 2, tid, s8);
+      }
       // tiles past the wave's last query are skipped (wave-uniform)
       if (wave_live && 64 * j <= qlast) {
-        // score multiplier; kept >= 1e-30 so that masked keys (-inf) stay
-        // -inf when a group's K scale is 0 (its scores are then ~0, as they
-        // should be)
-        const float c = __builtin_fmaxf(
-            (64 * j < a.committed ? h2f(a.ksc[j * NKV + g]) : 1.0f) * a.qscale, 1e-30f);
-        // ---- S^T = K Q^T: Sc[kt][qt] rows = keys 16 kt + 4 b + i, column = query n
-        f32x4 Sc[4][2];
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-          Sc[kt][0] = Sc[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kb = 0; kb < 2; kb++) {
-            const f16x8 kop = *(const f16x8*)(kt_lds + pf_kaddr(16 * kt + n, 4 * kb + b));
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++)
-              Sc[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[qt][kb], Sc[kt][qt], 0, 0, 0);
-          }
-        }
-        // ---- causal mask (only tiles that reach past the wave's first query)
-        const bool diag = 64 * j + 63 > qmin;
-        if (diag) {
-#pragma unroll
-          for (int qt = 0; qt < 2; qt++) {
-            const int qpos = a.past + q0 + 16 * qt + n;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-              for (int i = 0; i < 4; i++)
-                if (64 * j + 16 * kt + 4 * b + i > qpos) Sc[kt][qt][i] = -__builtin_inff();
-          }
-        }
-        // ---- tile max per query column, lazily moved running max
-        float mt[2];
-        bool need[2];
-#pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
-          float cm = __builtin_fmaxf(__builtin_fmaxf(Sc[0][qt][0], Sc[0][qt][1]),
-                                     __builtin_fmaxf(Sc[0][qt][2], Sc[0][qt][3]));
-#pragma unroll
-          for (int kt = 1; kt < 4; kt++)
-            cm = __builtin_fmaxf(cm, __builtin_fmaxf(__builtin_fmaxf(Sc[kt][qt][0], Sc[kt][qt][1]),
-                                                     __builtin_fmaxf(Sc[kt][qt][2], Sc[kt][qt][3])));
-          cm = __builtin_fmaxf(cm, __shfl_xor(cm, 16));
-          cm = __builtin_fmaxf(cm, __shfl_xor(cm, 32));
-          mt[qt] = cm == -__builtin_inff() ? cm : cm * c;
-          need[qt] = mt[qt] > mrun[qt] + kPfLazy;
-        }
-        if (__any(need[0] || need[1])) {
-#pragma unroll
-          for (int qt = 0; qt < 2; qt++) {
-            const float corr = need[qt] ? __builtin_amdgcn_exp2f(mrun[qt] - mt[qt]) : 1.0f;
-            if (need[qt]) mrun[qt] = mt[qt];
-            lrun[qt] *= corr;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-              for (int i = 0; i < 4; i++) O[dt][qt][i] *= corr;
-          }
-        }
-        // ---- P (fp16), row sums, O^T += V^T P^T
-        f16x8 pop[2][2];  // [key block u][qt]
-#pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
-          const float nm = -mrun[qt];
-#pragma unroll
-          for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-              pop[kt >> 1][qt][4 * (kt & 1) + i] =
-                  (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(Sc[kt][qt][i], c, nm));
-          float rs = lrun[qt];
-#pragma unroll
-          for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-              rs = __builtin_amdgcn_fdot2(f16x2{pop[u][qt][2 * e], pop[u][qt][2 * e + 1]},
-                                          f16x2{(_Float16)1.0f, (_Float16)1.0f}, rs, false);
-          lrun[qt] = rs;
-        }
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-          for (int u = 0; u < 2; u++) {
-            const f16x8 vop = *(const f16x8*)(vt_lds + pf_vaddr(16 * dt + n, 32 * u + 8 * b));
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++)
-              O[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[u][qt], O[dt][qt], 0, 0, 0);
-          }
+        const float c = __builtin_fmaxf(c_cur * a.qscale, 1e-30f);
+        if (64 * j + 63 > qmin)
+          pf_tile<true>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, 64 * j, qpos0, n, b, O,
+                        mrun, lrun);
+        else
+          pf_tile<false>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, 64 * j, qpos0, n, b, O,
+                         mrun, lrun);
       }
-      if (j + 1 < ntile) pf_store(lds[(j + 1) & 1], tid, st);
+      c_cur = c_next;
+      __syncthreads();
+    }
+    if (ntile > nf) {
+      PfStage16 s16;
+      pf_load16(a, g, nvalid_tail, tid, s16);
+      pf_store16(lds[nf & 1], tid, s16);
+      __syncthreads();
+      if (wave_live && 64 * nf <= qlast)
+        pf_tile<true>(lds[nf & 1], lds[nf & 1] + kPfTileBytes, qop,
+                      __builtin_fmaxf(a.qscale, 1e-30f), 64 * nf, qpos0, n, b, O, mrun, lrun);
       __syncthreads();
     }
     // ---- normalise and store: lane holds query q0 + 16 qt + n, dims 16 dt + 4 b .. +3
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
-      float L = lrun[qt];
-      L += __shfl_xor(L, 16);
-      L += __shfl_xor(L, 32);
+      const float L = pf_colsum(lrun[qt]);
       const int s = q0 + 16 * qt + n;
       if (s < a.S) {
         const float inv = 1.0f / L;
