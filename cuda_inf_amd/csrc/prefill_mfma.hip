@@ -39,7 +39,6 @@ constexpr int kPfWaves = 8;
 constexpr int kPfQ = 64;            // queries per block
 constexpr int kPfTileBytes = 8192;  // one fp16 64 x 64 tile
 constexpr float kPfLog2e = 1.44269504088896340736f;
-constexpr float kPfLazy = 8.0f;     // log2 headroom before the running max moves
 
 struct PrefillArgs {
   const uint16_t* q;  // [S][32][64]
@@ -115,22 +114,23 @@ __device__ __forceinline__ void pf_load16(const PrefillArgs& a, int g, int nvali
     st.v1 = *(const u32x2*)(a.vtail + ((size_t)(2 * kp + 1) * NKV + g) * D + 4 * dc);
 }
 
-// K row chunk and the V^T words of this thread; the upper half-wave writes
-// its dims in the order 1,0,3,2 (spreads the writes over all LDS banks)
-__device__ __forceinline__ void pf_store(uint8_t* buf, int tid, u32x4 kw, f16x4 va, f16x4 vb) {
+// K row chunk and the V^T words of this thread (dims 4dc..4dc+3, each the
+// pair key 2kp, key 2kp+1).  The upper half-wave writes its dims in the
+// order 1,0,3,2, which spreads the writes over all LDS banks: the byte
+// selectors sel01 / sel10 pick dims (0,1) / (1,0) of a pair of f16x2 words.
+__device__ __forceinline__ void pf_store(uint8_t* buf, int tid, u32x4 kw, u32x2 va, u32x2 vb,
+                                         uint32_t sel01, uint32_t sel10) {
   const int kkey = tid >> 3, kch = tid & 7, kp = tid & 31, dc = tid >> 5;
   *(u32x4*)(buf + pf_kaddr(kkey, kch)) = kw;
   const int slot = pf_vslot(2 * kp);
   const int flip = (tid >> 5) & 1;
   uint8_t* vt = buf + kPfTileBytes;
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const _Float16 x0 = flip ? va[e ^ 1] : va[e];
-    const _Float16 x1 = flip ? vb[e ^ 1] : vb[e];
-    const uint32_t word = (uint32_t)__builtin_bit_cast(uint16_t, x0) |
-                          ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
-    *(uint32_t*)(vt + pf_vaddr(4 * dc + (e ^ flip), slot)) = word;
-  }
+  // word for dim 4dc + d: (va half d, vb half d); v_perm picks bytes of
+  // {vb, va} (va = bytes 0-3, vb = bytes 4-7)
+  *(uint32_t*)(vt + pf_vaddr(4 * dc + (0 ^ flip), slot)) = __builtin_amdgcn_perm(vb[0], va[0], sel01);
+  *(uint32_t*)(vt + pf_vaddr(4 * dc + (1 ^ flip), slot)) = __builtin_amdgcn_perm(vb[0], va[0], sel10);
+  *(uint32_t*)(vt + pf_vaddr(4 * dc + (2 ^ flip), slot)) = __builtin_amdgcn_perm(vb[1], va[1], sel01);
+  *(uint32_t*)(vt + pf_vaddr(4 * dc + (3 ^ flip), slot)) = __builtin_amdgcn_perm(vb[1], va[1], sel10);
 }
 
 // A group scale loaded two tiles ahead, read when its tile is staged.  The
@@ -142,12 +142,13 @@ __device__ __forceinline__ uint32_t pf_late(uint16_t x) {
   asm volatile("" : "+v"(v));
   return v;
 }
-// K scale -> score multiplier base (times scale * log2e later); scores of a
-// group whose K scale is 0 are 0, and the multiplier is kept >= 1e-30 where
-// it is used so that masked keys (-inf) stay -inf
+
+// K scale -> score multiplier base (times scale * log2e where it is used)
 __device__ __forceinline__ float pf_scale(uint16_t ks) { return h2f((uint16_t)pf_late(ks)); }
 
-__device__ __forceinline__ void pf_store8(uint8_t* buf, int tid, const PfStage8& st) {
+// K is staged exactly (fp8 -> fp16), V as V * V scale (one fp16 rounding)
+__device__ __forceinline__ void pf_store8(uint8_t* buf, int tid, const PfStage8& st,
+                                          uint32_t sel01, uint32_t sel10) {
   const u32x4 kw = __builtin_bit_cast(u32x4, pf_cvt8(st.k[0], st.k[1]));
   const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)pf_late(st.vs));
   const f16x2 s2 = f16x2{s, s};
@@ -155,11 +156,14 @@ __device__ __forceinline__ void pf_store8(uint8_t* buf, int tid, const PfStage8&
   const f16x2 a1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v0, 1.0f, true) * s2;
   const f16x2 b0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1, 1.0f, false) * s2;
   const f16x2 b1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.v1, 1.0f, true) * s2;
-  pf_store(buf, tid, kw, f16x4{a0[0], a0[1], a1[0], a1[1]}, f16x4{b0[0], b0[1], b1[0], b1[1]});
+  pf_store(buf, tid, kw,
+           u32x2{__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1)},
+           u32x2{__builtin_bit_cast(uint32_t, b0), __builtin_bit_cast(uint32_t, b1)}, sel01, sel10);
 }
 
-__device__ __forceinline__ void pf_store16(uint8_t* buf, int tid, const PfStage16& st) {
-  pf_store(buf, tid, st.k, __builtin_bit_cast(f16x4, st.v0), __builtin_bit_cast(f16x4, st.v1));
+__device__ __forceinline__ void pf_store16(uint8_t* buf, int tid, const PfStage16& st,
+                                           uint32_t sel01, uint32_t sel10) {
+  pf_store(buf, tid, st.k, st.v0, st.v1, sel01, sel10);
 }
 
 // max over the 4 lanes {l, l^16, l^32, l^48} that hold one query column
@@ -172,42 +176,40 @@ __device__ __forceinline__ float pf_colsum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// Softmax numerators of one 16-query tile: S[kt] rows = keys 64j + 16kt +
-// 4b + i, column = query qpos.  P[u] is the B operand of key block u.
-// Returns the largest exponent used (log2 units above the running max).
+// Softmax numerators of one 16-query tile: exponents s * c - m (log2
+// units) of the scores S[kt] (rows = keys key0 + 16 kt + i, column = query
+// qpos).  P[u] is the B operand of key block u; returns this lane's sum of
+// the fp16 numerators, which is infinite once a numerator overflows fp16,
+// i.e. once a score exceeds the running max by about 16.
 template <bool kMask>
 __device__ __forceinline__ float pf_exp(const f32x4 (&S)[4], float c, float m, int key0, int qpos,
-                                        f16x8 (&P)[2], float& rs) {
-  float tm = -__builtin_inff();
-  rs = 0.f;
+                                        f16x8 (&P)[2]) {
 #pragma unroll
-  for (int kt = 0; kt < 4; kt++) {
-    float t[4];
+  for (int kt = 0; kt < 4; kt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      t[i] = __builtin_fmaf(S[kt][i], c, -m);
-      if (kMask && key0 + 16 * kt + i > qpos) t[i] = -__builtin_inff();
+      float t = __builtin_fmaf(S[kt][i], c, -m);
+      if (kMask && key0 + 16 * kt + i > qpos) t = -__builtin_inff();
+      P[kt >> 1][4 * (kt & 1) + i] = (_Float16)__builtin_amdgcn_exp2f(t);
     }
-    tm = __builtin_fmaxf(tm, __builtin_fmaxf(__builtin_fmaxf(t[0], t[1]), __builtin_fmaxf(t[2], t[3])));
-#pragma unroll
-    for (int i = 0; i < 4; i++) P[kt >> 1][4 * (kt & 1) + i] = (_Float16)__builtin_amdgcn_exp2f(t[i]);
-  }
   const f16x2 one = f16x2{(_Float16)1.0f, (_Float16)1.0f};
+  float rs = 0.f;
 #pragma unroll
   for (int u = 0; u < 2; u++)
 #pragma unroll
     for (int e = 0; e < 4; e++)
       rs = __builtin_amdgcn_fdot2(f16x2{P[u][2 * e], P[u][2 * e + 1]}, one, rs, false);
-  return tm;
+  return rs;
 }
 
-// Tile max above the running max beyond the headroom (rare after the first
-// tiles): move the running max to the column's tile max, rescale O and l,
-// recompute P.
+// Moves the running max of a query column to the column's largest score of
+// this tile: always on the column's first tile (no max yet), otherwise when
+// that score is above it (a numerator overflowed).  Rescales O and l and
+// recomputes the numerators.
 template <bool kMask>
-__device__ __forceinline__ void pf_remax(const f32x4 (&S)[4], float c, float& m, float& l,
-                                         f32x4 (&O)[4], int key0, int qpos, f16x8 (&P)[2],
-                                         float& rs) {
+__device__ __forceinline__ float pf_remax(const f32x4 (&S)[4], float c, bool first, float& m,
+                                          float& l, f32x4 (&O)[4], int key0, int qpos,
+                                          f16x8 (&P)[2]) {
   float cm = -__builtin_inff();
 #pragma unroll
   for (int kt = 0; kt < 4; kt++)
@@ -216,10 +218,12 @@ __device__ __forceinline__ void pf_remax(const f32x4 (&S)[4], float c, float& m,
       const bool out = kMask && key0 + 16 * kt + i > qpos;
       cm = __builtin_fmaxf(cm, out ? -__builtin_inff() : S[kt][i]);
     }
-  cm = pf_colmax(cm);
-  const float mt = cm == -__builtin_inff() ? cm : cm * c;
-  if (mt > m + kPfLazy) {
-    const float corr = __builtin_amdgcn_exp2f(m - mt);  // 0 on the first tile
+  // finite on a first tile (key 0 is never masked); c > 0
+  const float mt = pf_colmax(cm) * c;
+  if (first) {
+    m = mt;
+  } else if (mt > m) {
+    const float corr = __builtin_amdgcn_exp2f(m - mt);
     m = mt;
     l *= corr;
 #pragma unroll
@@ -227,18 +231,35 @@ __device__ __forceinline__ void pf_remax(const f32x4 (&S)[4], float c, float& m,
 #pragma unroll
       for (int i = 0; i < 4; i++) O[dt][i] *= corr;
   }
-  pf_exp<kMask>(S, c, m, key0, qpos, P, rs);
+  return pf_exp<kMask>(S, c, m, key0, qpos, P);
 }
 
-// One 64-key tile for the wave's two 16-query tiles.  The second tile's
-// matrix products are issued before the first tile's exponentials, and the
+// exponentials of one query tile, with the re-max path when needed.  The
+// running max only moves when a numerator would overflow fp16, so between
+// moves the exponents stay below 16 (fp16 numerators, fp32 sums are safe).
+template <bool kMask>
+__device__ __forceinline__ void pf_softmax(const f32x4 (&S)[4], float c, bool first, int key0,
+                                           int qpos, float& m, float& l, f32x4 (&O)[4][2],
+                                           int qt, f16x8 (&P)[2]) {
+  float rs = first ? __builtin_inff() : pf_exp<kMask>(S, c, m, key0, qpos, P);
+  if (__any(!(rs < 3.0e38f))) {
+    f32x4 Oq[4] = {O[0][qt], O[1][qt], O[2][qt], O[3][qt]};
+    rs = pf_remax<kMask>(S, c, first, m, l, Oq, key0, qpos, P);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) O[dt][qt] = Oq[dt];
+  }
+  l += rs;
+}
+
+// One 64-key tile for the wave's two 16-query tiles.  The second query
+// tile's products are issued before the first tile's exponentials, and the
 // first tile's P V before the second tile's exponentials, so the matrix
 // cores and the vector unit of one wave overlap.
 template <bool kMask>
 __device__ __forceinline__ void pf_tile(const uint8_t* kt_lds, const uint8_t* vt_lds,
-                                        const f16x8 (&qop)[2][2], float c, int key0, int qpos0,
-                                        int n, int b, f32x4 (&O)[4][2], float (&mrun)[2],
-                                        float (&lrun)[2]) {
+                                        const f16x8 (&qop)[2][2], float c, bool first, int key0,
+                                        int qpos0, int n, int b, f32x4 (&O)[4][2],
+                                        float (&mrun)[2], float (&lrun)[2]) {
   f16x8 kop[4][2];
 #pragma unroll
   for (int kt = 0; kt < 4; kt++)
@@ -258,15 +279,7 @@ __device__ __forceinline__ void pf_tile(const uint8_t* kt_lds, const uint8_t* vt
   }
   const int kb0 = key0 + 4 * b;
   f16x8 P0[2], P1[2];
-  float rs0, rs1;
-  float tm = pf_exp<kMask>(S0, c, mrun[0], kb0, qpos0, P0, rs0);
-  if (__any(tm > kPfLazy)) {
-    f32x4 Oq[4] = {O[0][0], O[1][0], O[2][0], O[3][0]};
-    pf_remax<kMask>(S0, c, mrun[0], lrun[0], Oq, kb0, qpos0, P0, rs0);
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) O[dt][0] = Oq[dt];
-  }
-  lrun[0] += rs0;
+  pf_softmax<kMask>(S0, c, first, kb0, qpos0, mrun[0], lrun[0], O, 0, P0);
   f16x8 vop[4][2];
 #pragma unroll
   for (int dt = 0; dt < 4; dt++)
@@ -278,14 +291,7 @@ __device__ __forceinline__ void pf_tile(const uint8_t* kt_lds, const uint8_t* vt
 #pragma unroll
     for (int u = 0; u < 2; u++)
       O[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[dt][u], P0[u], O[dt][0], 0, 0, 0);
-  tm = pf_exp<kMask>(S1, c, mrun[1], kb0, qpos0 + 16, P1, rs1);
-  if (__any(tm > kPfLazy)) {
-    f32x4 Oq[4] = {O[0][1], O[1][1], O[2][1], O[3][1]};
-    pf_remax<kMask>(S1, c, mrun[1], lrun[1], Oq, kb0, qpos0 + 16, P1, rs1);
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) O[dt][1] = Oq[dt];
-  }
-  lrun[1] += rs1;
+  pf_softmax<kMask>(S1, c, first, kb0, qpos0 + 16, mrun[1], lrun[1], O, 1, P1);
 #pragma unroll
   for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -301,6 +307,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
   const int h = g * GQA + (w & 3);
   const int nvalid_tail = a.past + a.S - a.committed;  // tail keys 0..63
   const int nfp8 = a.committed >> 6;
+  // v_perm selectors of this lane's V^T word pairs (see pf_store)
+  const uint32_t sel01 = ((tid >> 5) & 1) ? 0x07060302u : 0x05040100u;
+  const uint32_t sel10 = ((tid >> 5) & 1) ? 0x05040100u : 0x07060302u;
 
   for (int phase = 0; phase < 2; phase++) {
     const int blk = phase == 0 ? a.nblk - 1 - pr : pr;
@@ -338,11 +347,11 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
     const int nf = min(ntile, nfp8);
     const int qpos0 = a.past + q0 + n;
     PfStage8 s8;
-    float c_cur = 1.0f, c_next = 1.0f;
+    float c_cur = 1.0f, c_next = 1.0f;  // K scale of the tile being computed / staged
     if (nf > 0) {
       pf_load8(a, g, 0, tid, s8);
       c_cur = pf_scale(s8.ks);
-      pf_store8(lds[0], tid, s8);
+      pf_store8(lds[0], tid, s8, sel01, sel10);
       if (nf > 1) pf_load8(a, g, 1, tid, s8);
     }
     __syncthreads();
@@ -351,18 +360,21 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
       // start loading tile j+2
       if (j + 1 < nf) {
         c_next = pf_scale(s8.ks);
-        pf_store8(lds[(j + 1) & 1], tid, s8);
+        pf_store8(lds[(j + 1) & 1], tid, s8, sel01, sel10);
         if (j + 2 < nf) pf_load8(a, g, j + 2, tid, s8);
       }
-      // tiles past the wave's last query are skipped (wave-uniform)
+      // tiles past the wave's last query are skipped (wave-uniform).  The
+      // score multiplier is kept >= 1e-30 so that masked keys (-inf) stay
+      // -inf when a group's K scale is 0 (its scores are then ~0, as they
+      // should be).
       if (wave_live && 64 * j <= qlast) {
         const float c = __builtin_fmaxf(c_cur * a.qscale, 1e-30f);
         if (64 * j + 63 > qmin)
-          pf_tile<true>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, 64 * j, qpos0, n, b, O,
-                        mrun, lrun);
+          pf_tile<true>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, j == 0, 64 * j, qpos0, n,
+                        b, O, mrun, lrun);
         else
-          pf_tile<false>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, 64 * j, qpos0, n, b, O,
-                         mrun, lrun);
+          pf_tile<false>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, j == 0, 64 * j, qpos0,
+                         n, b, O, mrun, lrun);
       }
       c_cur = c_next;
       __syncthreads();
@@ -370,11 +382,12 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
     if (ntile > nf) {
       PfStage16 s16;
       pf_load16(a, g, nvalid_tail, tid, s16);
-      pf_store16(lds[nf & 1], tid, s16);
+      pf_store16(lds[nf & 1], tid, s16, sel01, sel10);
       __syncthreads();
       if (wave_live && 64 * nf <= qlast)
         pf_tile<true>(lds[nf & 1], lds[nf & 1] + kPfTileBytes, qop,
-                      __builtin_fmaxf(a.qscale, 1e-30f), 64 * nf, qpos0, n, b, O, mrun, lrun);
+                      __builtin_fmaxf(a.qscale, 1e-30f), nf == 0, 64 * nf, qpos0, n, b, O, mrun,
+                      lrun);
       __syncthreads();
     }
     // ---- normalise and store: lane holds query q0 + 16 qt + n, dims 16 dt + 4 b .. +3
