@@ -119,6 +119,57 @@ __device__ __forceinline__ float fast_exp(float x) {
 }
 
 // ---------------------------------------------------------------- waves
+// Cross-lane steps without the LDS unit: DPP row rotations within each
+// 16-lane row, then v_permlane16_swap / v_permlane32_swap across rows (each
+// returns, per lane, its own value and that of lane l ^ 16 / l ^ 32).
+template <int kN>
+__device__ __forceinline__ float row_ror(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x120 + kN, 0xF, 0xF, false));
+}
+__device__ __forceinline__ f32x2 swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return f32x2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ f32x2 swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return f32x2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+// max / sum over the lanes {l, l^16, l^32, l^48} (one MFMA column)
+__device__ __forceinline__ float col4_max(float v) {
+  f32x2 r = swap16(v);
+  v = __builtin_fmaxf(r[0], r[1]);
+  r = swap32(v);
+  return __builtin_fmaxf(r[0], r[1]);
+}
+__device__ __forceinline__ float col4_sum(float v) {
+  f32x2 r = swap16(v);
+  v = r[0] + r[1];
+  r = swap32(v);
+  return r[0] + r[1];
+}
+// max over the wave (exact in any order)
+__device__ __forceinline__ float wave_max_fast(float v) {
+  v = __builtin_fmaxf(v, row_ror<8>(v));
+  v = __builtin_fmaxf(v, row_ror<4>(v));
+  v = __builtin_fmaxf(v, row_ror<2>(v));
+  v = __builtin_fmaxf(v, row_ror<1>(v));
+  return col4_max(v);
+}
+// sum over the wave (every lane gets the same value; the order differs from
+// wave_sum's butterfly, so this is not for the deterministic mass)
+__device__ __forceinline__ float wave_sum_fast(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return col4_sum(v);
+}
+
+// butterfly max / sum (xor 32, 16, ..., 1): the fixed order of the
+// deterministic attention mass
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off));

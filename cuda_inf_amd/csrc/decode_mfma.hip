@@ -156,8 +156,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
         S[t][i] *= ksc;
         rmx = __builtin_fmaxf(rmx, S[t][i]);
       }
-    rmx = __builtin_fmaxf(rmx, __shfl_xor(rmx, 16));
-    rmx = __builtin_fmaxf(rmx, __shfl_xor(rmx, 32));
+    rmx = col4_max(rmx);
     const float mnew = __builtin_fmaxf(mx, rmx);
     const float corr = __builtin_amdgcn_exp2f(mx - mnew);  // rescales earlier rounds
     mx = mnew;
@@ -171,8 +170,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
         P[t * 4 + i] = ph;
         rs += (float)ph;
       }
-    rs += __shfl_xor(rs, 16);
-    rs += __shfl_xor(rs, 32);
+    rs = col4_sum(rs);
     lsum = __builtin_fmaf(lsum, corr, rs);
     // this lane's O rows are (kv head b, query head i); the correction of
     // column (b, i) lives in lane 4b + i
@@ -305,7 +303,7 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     x = sacc * (a.scale * kLog2e);
   }
   // ---- one softmax over tail keys and partials
-  const float M = wave_max(__builtin_fmaxf(x, __builtin_fmaxf(pm[0], pm[1])));
+  const float M = wave_max_fast(__builtin_fmaxf(x, __builtin_fmaxf(pm[0], pm[1])));
   const float pt = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
   float L = pt, o[8];
 #pragma unroll
@@ -323,9 +321,9 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
       o[4 + e] = __builtin_fmaf(po[u][1][e], wgt, o[4 + e]);
     }
   }
-  L = wave_sum(L);
+  L = wave_sum_fast(L);
 #pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = wave_sum(o[e]);
+  for (int e = 0; e < 8; e++) o[e] = wave_sum_fast(o[e]);
   if (l == 0) {
     const float inv = 1.f / L;
     u32x4 r;

@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void k_commit_group(const uint16_t* __restrict
     mk = __builtin_fmaxf(mk, __builtin_fabsf(kf[i]));
     mv = __builtin_fmaxf(mv, __builtin_fabsf(vf[i]));
   }
-  mk = wave_max(mk);
-  mv = wave_max(mv);
+  mk = wave_max_fast(mk);
+  mv = wave_max_fast(mv);
   __shared__ float red[2][4];
   const int w = t >> 6;
   if ((t & 63) == 0) { red[0][w] = mk; red[1][w] = mv; }
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64) void k_quant_write(const uint16_t* __restrict__
   const int jh = blockIdx.x, j = jh / NKV, h = jh % NKV, d = threadIdx.x;
   const size_t src = ((size_t)j * NKV + h) * D + d;
   const float kv = h2f(k[src]), vv = h2f(v[src]);
-  const float mk = wave_max(__builtin_fabsf(kv)), mv = wave_max(__builtin_fabsf(vv));
+  const float mk = wave_max_fast(__builtin_fabsf(kv)), mv = wave_max_fast(__builtin_fabsf(vv));
   const float sck = quant_scale(mk), scv = quant_scale(mv);
   const int slot = dst_slots[j];
   // pack 4 neighbouring lanes' bytes into one dword store

@@ -167,14 +167,8 @@ __device__ __forceinline__ void pf_store16(uint8_t* buf, int tid, const PfStage1
 }
 
 // max over the 4 lanes {l, l^16, l^32, l^48} that hold one query column
-__device__ __forceinline__ float pf_colmax(float v) {
-  v = __builtin_fmaxf(v, __shfl_xor(v, 16));
-  return __builtin_fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float pf_colsum(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
-}
+__device__ __forceinline__ float pf_colmax(float v) { return col4_max(v); }
+__device__ __forceinline__ float pf_colsum(float v) { return col4_sum(v); }
 
 // Softmax numerators of one 16-query tile: exponents s * c - m (log2
 // units) of the scores S[kt] (rows = keys key0 + 16 kt + i, column = query
