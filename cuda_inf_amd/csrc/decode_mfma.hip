@@ -62,10 +62,10 @@ __device__ __forceinline__ int vaddr(int key, int c) { return key * 256 + ((c ^ 
 
 struct DecodeArgs {
   const uint16_t* q;  // [32][64]
-  const uint8_t* kc8;
-  const uint8_t* vc8;
-  const uint16_t* ksc;
-  const uint16_t* vsc;
+  uint8_t* kc8;    // written only when the fresh token completes a group
+  uint8_t* vc8;
+  uint16_t* ksc;
+  uint16_t* vsc;
   uint16_t* ktail;
   uint16_t* vtail;
   const uint16_t* knew;  // fresh token [8][64] (key qpos), or null: it is in the tail
@@ -268,19 +268,26 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
       po[u][0] = po[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  u32x4 kq[8], qq[8], vv = u32x4{0u, 0u, 0u, 0u};
+  u32x4 kq[8], qq[8], vrow[8], vv = u32x4{0u, 0u, 0u, 0u};
   const bool live = l < ntail;
+  // the fresh token completes the group: commit it in this launch
+  const bool commit = a.knew && ntail == G;
   if (live) {
     const bool fresh = a.knew && l == ntail - 1;
     const uint16_t* kp = fresh ? a.knew + kvh * D : a.ktail + ((size_t)l * NKV + kvh) * D;
-    const uint16_t* vp = (fresh ? a.vnew + kvh * D : a.vtail + ((size_t)l * NKV + kvh) * D) + 8 * c;
+    const uint16_t* vp = fresh ? a.vnew + kvh * D : a.vtail + ((size_t)l * NKV + kvh) * D;
     const uint16_t* qp = a.q + (size_t)h * D;
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) {
       kq[cc] = *(const u32x4*)(kp + 8 * cc);
       qq[cc] = *(const u32x4*)(qp + 8 * cc);
     }
-    vv = *(const u32x4*)vp;
+    if (commit) {
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) vrow[cc] = *(const u32x4*)(vp + 8 * cc);
+    } else {
+      vv = *(const u32x4*)(vp + 8 * c);
+    }
   }
   // the fresh token joins the tail, written once per kv head
   if (a.knew && c == 0 && h % GQA == 0 && l < 16) {
@@ -289,28 +296,93 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     const uint16_t* src = (l < 8 ? a.knew : a.vnew) + kvh * D + cc * 8;
     *(u32x4*)dst = *(const u32x4*)src;
   }
-  // ---- tail scores (log2 units)
-  float x = -1e30f;
-  if (live) {
-    float sacc = 0.f;
+  // ---- tail scores (log2 units) and this lane's V values (dims 8c..8c+7)
+  float x = -1e30f, vf[8];
+  if (!commit) {
+    if (live) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sacc = __builtin_fmaf(h2f((uint16_t)qq[cc][i]), h2f((uint16_t)kq[cc][i]), sacc);
+          sacc = __builtin_fmaf(h2f((uint16_t)(qq[cc][i] >> 16)), h2f((uint16_t)(kq[cc][i] >> 16)), sacc);
+        }
+      x = sacc * (a.scale * kLog2e);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      vf[2 * i] = h2f((uint16_t)vv[i]);
+      vf[2 * i + 1] = h2f((uint16_t)(vv[i] >> 16));
+    }
+  } else {
+    // The fresh token fills the group: it is committed (kv_commit_group,
+    // engine.cu:202-228) and, as in the reference, the group is attended in
+    // its FP8 form.  Every wave of the kv head quantises what it needs; the
+    // wave (c 0, first query head) writes the bytes and the scales.
+    float kf[64], vfl[64];
 #pragma unroll
     for (int cc = 0; cc < 8; cc++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        sacc = __builtin_fmaf(h2f((uint16_t)qq[cc][i]), h2f((uint16_t)kq[cc][i]), sacc);
-        sacc = __builtin_fmaf(h2f((uint16_t)(qq[cc][i] >> 16)), h2f((uint16_t)(kq[cc][i] >> 16)), sacc);
+        kf[8 * cc + 2 * i] = h2f((uint16_t)kq[cc][i]);
+        kf[8 * cc + 2 * i + 1] = h2f((uint16_t)(kq[cc][i] >> 16));
+        vfl[8 * cc + 2 * i] = h2f((uint16_t)vrow[cc][i]);
+        vfl[8 * cc + 2 * i + 1] = h2f((uint16_t)(vrow[cc][i] >> 16));
       }
+    float ak = 0.f, av = 0.f;
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      ak = __builtin_fmaxf(ak, __builtin_fabsf(kf[d]));
+      av = __builtin_fmaxf(av, __builtin_fabsf(vfl[d]));
+    }
+    const float sck = quant_scale(wave_max_fast(ak)), scv = quant_scale(wave_max_fast(av));
+    const uint16_t skh = f2h(sck), svh = f2h(scv);
+    const float kdq = h2f(skh), vdq = h2f(svh);
+    const bool writer = c == 0 && h % GQA == 0;
+    const size_t row = ((size_t)(a.committed + l) * NKV + kvh) * D;
+    float sacc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const uint32_t kb = e4m3x4(kf[4 * j] / sck, kf[4 * j + 1] / sck, kf[4 * j + 2] / sck,
+                                 kf[4 * j + 3] / sck);
+      sacc = __builtin_fmaf(h2f((uint16_t)(qq[j >> 1][(j & 1) * 2] & 0xFFFF)),
+                            e4m3_to_f32<0>(kb) * kdq, sacc);
+      sacc = __builtin_fmaf(h2f((uint16_t)(qq[j >> 1][(j & 1) * 2] >> 16)),
+                            e4m3_to_f32<1>(kb) * kdq, sacc);
+      sacc = __builtin_fmaf(h2f((uint16_t)(qq[j >> 1][(j & 1) * 2 + 1] & 0xFFFF)),
+                            e4m3_to_f32<2>(kb) * kdq, sacc);
+      sacc = __builtin_fmaf(h2f((uint16_t)(qq[j >> 1][(j & 1) * 2 + 1] >> 16)),
+                            e4m3_to_f32<3>(kb) * kdq, sacc);
+      if (writer) *(uint32_t*)(a.kc8 + row + 4 * j) = kb;
+    }
     x = sacc * (a.scale * kLog2e);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint32_t vb = e4m3x4(vfl[8 * c + 4 * j] / scv, vfl[8 * c + 4 * j + 1] / scv,
+                                 vfl[8 * c + 4 * j + 2] / scv, vfl[8 * c + 4 * j + 3] / scv);
+      vf[4 * j] = e4m3_to_f32<0>(vb) * vdq;
+      vf[4 * j + 1] = e4m3_to_f32<1>(vb) * vdq;
+      vf[4 * j + 2] = e4m3_to_f32<2>(vb) * vdq;
+      vf[4 * j + 3] = e4m3_to_f32<3>(vb) * vdq;
+    }
+    if (writer) {
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        *(uint32_t*)(a.vc8 + row + 4 * j) =
+            e4m3x4(vfl[4 * j] / scv, vfl[4 * j + 1] / scv, vfl[4 * j + 2] / scv, vfl[4 * j + 3] / scv);
+      if (l == 0) {
+        a.ksc[(a.committed / G) * NKV + kvh] = skh;
+        a.vsc[(a.committed / G) * NKV + kvh] = svh;
+      }
+    }
   }
   // ---- one softmax over tail keys and partials
   const float M = wave_max_fast(__builtin_fmaxf(x, __builtin_fmaxf(pm[0], pm[1])));
   const float pt = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
   float L = pt, o[8];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    o[2 * i] = pt * h2f((uint16_t)vv[i]);
-    o[2 * i + 1] = pt * h2f((uint16_t)(vv[i] >> 16));
-  }
+  for (int e = 0; e < 8; e++) o[e] = pt * vf[e];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const float wgt = pl[u] > 0.f ? __builtin_amdgcn_exp2f(pm[u] - M) : 0.f;
@@ -373,7 +445,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   const int npairs = committed / 32;
   const int nwg = dec_nwg(npairs);
   if ((int64_t)NH * nwg * kPart * (int64_t)sizeof(float) > ws_bytes) return CIA_ERR_ARG;
-  DecodeArgs da{q, kc8, vc8, ksc, vsc, ktail, vtail, knew, vnew, committed, qpos, scale,
+  DecodeArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail, knew, vnew, committed, qpos, scale,
                 (float*)ws, npairs, nwg, out};
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_decode_attend, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);

@@ -244,14 +244,24 @@ int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int pa
   return CIA_OK;
 }
 
-// Single-token decode whose fresh token does not fill its group: the tail
-// write rides in the attention launch (no separate kv_write_tail launch).
+// Single-token decode on the matrix cores with the append fused in: the
+// fresh token's tail write, and the group commit when it completes the
+// group, ride in the attention launches (no kv_write_tail / kv_commit_group
+// launches).  Usable when the token lands in the current tail.
+bool fused_append_ok(const cia_layer* L, int past) {
+  const int slot = past - L->committed;
+  return L->nsplit == 0 && slot >= 0 && slot < CIA_KVGROUP && past < L->maxT &&
+         (slot < CIA_KVGROUP - 1 || L->committed + CIA_KVGROUP <= L->maxT);
+}
+
 int decode_fused_append(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         uint16_t* out, int past, float scale, void* stream,
                         void* mid_event = nullptr) {
-  return cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, k, v,
-                         L->committed, past, scale, out, L->ws_decode,
-                         cia_decode_workspace_bytes(L->maxT), stream, mid_event);
+  const int st = cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, k, v,
+                                 L->committed, past, scale, out, L->ws_decode,
+                                 cia_decode_workspace_bytes(L->maxT), stream, mid_event);
+  if (st == CIA_OK && past - L->committed == CIA_KVGROUP - 1) L->committed += CIA_KVGROUP;
+  return st;
 }
 
 }  // namespace
@@ -263,8 +273,7 @@ extern "C" int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t
   if (S < 1 || past < 0) return CIA_ERR_ARG;
   if (evicted) *evicted = -1;
   if (L->budget > 0) return h2o_forward(L, q, k, v, out, S, past, scale, evicted, stream);
-  if (S == 1 && L->nsplit == 0 && past - L->committed < CIA_KVGROUP - 1 &&
-      past >= L->committed && past < L->maxT)
+  if (S == 1 && fused_append_ok(L, past))
     return decode_fused_append(L, q, k, v, out, past, scale, stream);
   int st = group64_append(L, k, v, S, past, stream);
   if (st) return st;
@@ -294,8 +303,7 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
       cia_layer* L = &layers[l];
       const int pos = past + i;
       int st;
-      const bool fused = L->nsplit == 0 && pos >= L->committed &&
-                         pos - L->committed < CIA_KVGROUP - 1 && pos < L->maxT;
+      const bool fused = fused_append_ok(L, pos);
       if (!fused) {
         st = group64_append(L, k + r * krow, v + r * krow, 1, pos, stream);
         if (st) return st;

@@ -188,3 +188,69 @@ def test_decode_steps_through_commit(orc, cia, dev):
             _, r32, _ = orc.attn_decode(_u16(q), ref, pos, nsplit=16, nthreads=8)
             assert_close_f16(_u16(out)[0], r32, what=f"step {step} pos {pos}")
     assert L.committed == ref.committed
+    # the groups committed inside the decode launches are the reference's bytes
+    c = ref.committed
+    assert np.array_equal(L.kc8[:c].cpu().numpy().reshape(ref.kc8[:c].shape), ref.kc8[:c])
+    assert np.array_equal(L.vc8[:c].cpu().numpy().reshape(ref.vc8[:c].shape), ref.vc8[:c])
+    ng = c // 64
+    assert np.array_equal(_u16(L.ksc).reshape(-1, 8)[:ng], ref.ksc[:ng])
+    assert np.array_equal(_u16(L.vsc).reshape(-1, 8)[:ng], ref.vsc[:ng])
+    assert np.array_equal(_u16(L.ktail).reshape(ref.ktail.shape), ref.ktail)
+    assert np.array_equal(_u16(L.vtail).reshape(ref.vtail.shape), ref.vtail)
+
+
+def test_decode_loop_two_layers_through_commit(orc, cia, dev):
+    """cia_decode_loop (the bench's entry): 2 layers x 70 steps from 1990
+    tokens, crossing a group boundary; every 7th step and the commit steps are
+    checked against the oracle, then the caches byte for byte."""
+    import ctypes
+    from cuda_inf_amd import _lib
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    nL, n0, steps = 2, 1990, 70
+    layers, refs = [], []
+    for l in range(nL):
+        L = AttnLayer(n0 + steps + 64, nsplit=0, device=dev)
+        ref = orc.Group64Cache(n0 + steps + 64)
+        _, k0, v0 = qkv(n0, seed=20 + l, device="cpu", outliers=True)
+        k0d, v0d = k0.to(dev), v0.to(dev)  # alive until the append has run
+        _lib.call("cia_layer_append", ctypes.byref(L._s), k0d.data_ptr(), v0d.data_ptr(), n0, 0,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        ref.append(_u16(k0), _u16(v0), 0)
+        layers.append(L)
+        refs.append(ref)
+    torch.cuda.synchronize()
+    arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+    qs, ks, vs = [], [], []
+    for s in range(steps):
+        row = [qkv(1, seed=5000 + 10 * s + l, device="cpu", past=n0 + s, outliers=True)
+               for l in range(nL)]
+        qs.append(torch.cat([r[0] for r in row]))
+        ks.append(torch.cat([r[1] for r in row]))
+        vs.append(torch.cat([r[2] for r in row]))
+    q = torch.stack(qs).contiguous()       # [steps, nL, 32, 64]
+    k = torch.stack(ks).contiguous()       # [steps, nL, 8, 64]
+    v = torch.stack(vs).contiguous()
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = torch.empty_like(qd)
+    _lib.call("cia_decode_loop", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+              out.data_ptr(), n0, steps, 0.125, None, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = _u16(out)
+    for s in range(steps):
+        pos = n0 + s
+        for l in range(nL):
+            refs[l].append(_u16(k[s, l][None]), _u16(v[s, l][None]), pos)
+            if s % 7 == 0 or pos % 64 in (62, 63, 0):
+                _, r32, _ = orc.attn_decode(_u16(q[s, l][None]), refs[l], pos, nsplit=16, nthreads=8)
+                assert_close_f16(got[s, l], r32, what=f"step {s} layer {l}")
+    for l in range(nL):
+        c = refs[l].committed
+        assert arr[l].committed == c
+        L = layers[l]
+        assert np.array_equal(L.kc8[:c].cpu().numpy(), refs[l].kc8[:c])
+        assert np.array_equal(L.vc8[:c].cpu().numpy(), refs[l].vc8[:c])
+        assert np.array_equal(_u16(L.ksc)[:c // 64], refs[l].ksc[:c // 64])
+        assert np.array_equal(_u16(L.vsc)[:c // 64], refs[l].vsc[:c // 64])
+        assert np.array_equal(_u16(L.ktail), refs[l].ktail)
