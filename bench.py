@@ -60,6 +60,9 @@ def main():
                     help="HBM bytes per attend launch measured with rocprofv3 --pmc "
                          "(FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), reported as "
                          "roofline.traffic")
+    ap.add_argument("--long-ctx", type=int, default=131072,
+                    help="long-context decode leg: context tokens (0 = skip)")
+    ap.add_argument("--long-steps", type=int, default=8)
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="MiB: first run a plain device copy of this size three times "
                          "(the reference dispatch that scales rocprofv3 byte counters)")
@@ -224,10 +227,20 @@ def main():
                    "kernel": "attention_fused"}
         log(f"prefill {S}: {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s")
 
+    cpu_layer, cpu_committed = layers[0], arr[0].committed
+
+    # ---- long-context leg: matrix-core decode and the reference's split +
+    # combine at the split counts of the sweep
+    long_ctx = None
+    if a.long_ctx > 0:
+        del layers, arr
+        torch.cuda.empty_cache()
+        long_ctx = long_context_leg(a.long_ctx, nL, a.long_steps, dev, stream, log)
+
     # ---- CPU baseline: the oracle on this host's cores, one layer at a time
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline(layers[0], arr[0].committed, ctx + cur["step"] - 1, q, nL,
+        cpu = cpu_baseline(cpu_layer, cpu_committed, ctx + cur["step"] - 1, q, nL,
                            a.cpu_seconds, log)
 
     traffic = a.traffic if a.traffic is not None else measured_traffic(ctx, nL)
@@ -260,9 +273,68 @@ def main():
                      "event_bracketed_us": {"k_decode_attend": round(att_us, 3),
                                             "k_decode_finish": round(fin_us, 3)}},
         "prefill": prefill,
+        "long_context": long_ctx,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+
+def long_context_leg(ctx, nL, steps, dev, stream, log):
+    """Decode at ctx tokens (6 layers): the matrix-core path and the
+    reference's split + combine with 16, 64, 256 and 512 splits per head.
+    Each setting: 2 warm-up tokens, then `steps` timed tokens."""
+    import ctypes
+    import torch
+    from cuda_inf_amd import _lib, workload
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd._lib import D, NH, NKV, call
+    settings = [0, 16, 64, 256, 512]
+    total = len(settings) * (steps + 2)
+    layers = []
+    for l in range(nL):
+        L = AttnLayer(ctx + total + 64, nsplit=512, device=dev)
+        g = workload.generator(2000 + l, dev)
+        for c0 in range(0, ctx, 8192):
+            n = min(8192, ctx - c0)
+            k = workload.with_outliers(workload.normal_f16((n, NKV, D), g, dev), g)
+            v = workload.with_outliers(workload.normal_f16((n, NKV, D), g, dev), g)
+            call("cia_layer_append", ctypes.byref(L._s), k.data_ptr(), v.data_ptr(), n, c0,
+                 stream.cuda_stream)
+            torch.cuda.synchronize()
+        layers.append(L)
+    arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+    g = workload.generator(9, dev)
+    pos = torch.arange(ctx, ctx + total, device=dev)
+    q = workload.normal_f16((total, nL, NH, D), g, dev)
+    q = torch.stack([workload.prep_qk(q[:, l], pos) for l in range(nL)], dim=1).contiguous()
+    kk = workload.with_outliers(workload.normal_f16((total, nL, NKV, D), g, dev), g)
+    vv = workload.with_outliers(workload.normal_f16((total, nL, NKV, D), g, dev), g)
+    out = torch.empty((total, nL, NH, D), dtype=torch.float16, device=dev)
+    qrow, krow = nL * NH * D * 2, nL * NKV * D * 2
+    cur = 0
+    res = {"context": ctx, "layers": nL, "timed_tokens": steps}
+    for ns in settings:
+        for l in range(nL):
+            arr[l].nsplit = ns
+        times = []
+        for phase, n in (("warm", 2), ("timed", steps)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            call("cia_decode_loop", arr, nL, q.data_ptr() + cur * qrow, kk.data_ptr() + cur * krow,
+                 vv.data_ptr() + cur * krow, out.data_ptr() + cur * qrow, ctx + cur, n, 0.125,
+                 None, stream.cuda_stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            cur += n
+            if phase == "timed":
+                times.append(e0.elapsed_time(e1) * 1e3 / n)
+        us = times[0]
+        Tc = ((ctx + cur) // 64) * 64
+        gbps = algo_bytes(Tc, ctx + cur - Tc) * nL / (us * 1e-6) / 1e9
+        name = "matrix_core" if ns == 0 else f"split_{ns}"
+        res[name] = {"us_per_token": round(us, 2), "gbps": round(gbps, 1)}
+        log(f"long context {ctx}: {name}: {us:.1f} us/token, {gbps:.0f} GB/s")
+    return res
 
 
 def measured_traffic(ctx: int, nL: int):

@@ -234,9 +234,17 @@ def test_decode_loop_two_layers_through_commit(orc, cia, dev):
     v = torch.stack(vs).contiguous()
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     out = torch.empty_like(qd)
-    _lib.call("cia_decode_loop", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
-              out.data_ptr(), n0, steps, 0.125, None, torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
+    # three calls (graph replays after the first capture), eager work between
+    qrow, krow = nL * 32 * 64 * 2, nL * 8 * 64 * 2
+    s0 = 0
+    for n in (25, 20, 25):
+        _lib.call("cia_decode_loop", arr, nL, qd.data_ptr() + s0 * qrow, kd.data_ptr() + s0 * krow,
+                  vd.data_ptr() + s0 * krow, out.data_ptr() + s0 * qrow, n0 + s0, n, 0.125, None,
+                  torch.cuda.current_stream().cuda_stream)
+        (qd.float() * 2).sum().item()
+        torch.cuda.synchronize()
+        s0 += n
+    assert s0 == steps
     got = _u16(out)
     for s in range(steps):
         pos = n0 + s
