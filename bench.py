@@ -220,12 +220,23 @@ def main():
         p1.record(stream)
         torch.cuda.synchronize()
         pms = p0.elapsed_time(p1) / reps
+        # the whole layer step of the reference: append (FP8 commit of every
+        # full group, tail) and then the fused attention
+        p0.record(stream)
+        for _ in range(reps):
+            Lp._s.committed = 0
+            Lp.forward(qp, kp, vp, 0, out=outp)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        lms = p0.elapsed_time(p1) / reps
         flops = 4.0 * D * NH * S * (S + 1) / 2
         prefill = {"tokens": S, "us": round(pms * 1e3, 1),
                    "tflops": round(flops / (pms * 1e-3) / 1e12, 2),
                    "mfma_f16_frac": round(flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                   "kernel": "attention_fused"}
-        log(f"prefill {S}: {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s")
+                   "kernel": "attention_fused",
+                   "layer_us_with_append": round(lms * 1e3, 1)}
+        log(f"prefill {S}: attention {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s; "
+            f"append + attention {lms * 1e3:.1f} us")
 
     cpu_layer, cpu_committed = layers[0], arr[0].committed
 

@@ -10,6 +10,11 @@
 
 #include "cuda_inf_attn.h"
 
+extern "C" __attribute__((visibility("hidden"))) int cia_kv_append_batched(
+    const uint16_t* k, const uint16_t* v, uint16_t* ktail, uint16_t* vtail, uint8_t* kc8,
+    uint8_t* vc8, uint16_t* ksc, uint16_t* vsc, int* committed, int S, int past, int maxT,
+    void* stream);
+
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
@@ -190,32 +195,16 @@ int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16
                            S, past, scale, L->ws_mass, stream);
 }
 
-// placement loop (engine.cu:830-845): copy into the tail, commit full groups
+// placement loop (engine.cu:830-845): copy into the tail, commit full
+// groups -- one launch for all the groups the tokens complete and one for
+// the tail (the reference: one copy and one commit launch per group)
 int group64_append(cia_layer* L, const uint16_t* k, const uint16_t* v, int S, int past,
                    void* stream) {
   if (past + S > L->maxT) return CIA_ERR_ARG;
-  cia_append_op small[4];
-  std::vector<cia_append_op> big;
-  cia_append_op* ops = small;
-  const int max_ops = S / CIA_KVGROUP + 2;
-  if (max_ops > 4) {
-    big.resize(max_ops);
-    ops = big.data();
-  }
-  int n = 0, committed = L->committed;
-  int st = cia_kv_append_plan(&committed, S, past, ops, max_ops, &n);
+  int committed = L->committed;
+  const int st = cia_kv_append_batched(k, v, L->ktail, L->vtail, L->kc8, L->vc8, L->ksc, L->vsc,
+                                       &committed, S, past, L->maxT, stream);
   if (st) return st;
-  for (int i = 0; i < n; i++) {
-    const cia_append_op& op = ops[i];
-    const size_t off = (size_t)op.src_token * CIA_NKV * CIA_HEAD_DIM;
-    st = cia_kv_write_tail(k + off, v + off, L->ktail, L->vtail, op.slot, op.cnt, stream);
-    if (st) return st;
-    if (op.commit) {
-      st = cia_kv_commit_group(L->ktail, L->vtail, L->kc8, L->vc8, L->ksc, L->vsc,
-                               op.commit_base, op.commit_grp, stream);
-      if (st) return st;
-    }
-  }
   L->committed = committed;
   return CIA_OK;
 }

@@ -23,23 +23,30 @@ __global__ __launch_bounds__(256) void k_write_tail(const u32x4* __restrict__ k,
 }
 
 // ---------------------------------------------------------------- commit
-// grid = 8 kv heads, block = 256: thread t owns token t/4, dims
-// 16*(t%4) .. +15 of its head, for K and for V.
-__global__ __launch_bounds__(256) void k_commit_group(const uint16_t* __restrict__ ktail,
-                                                      const uint16_t* __restrict__ vtail,
-                                                      uint8_t* __restrict__ kc8,
-                                                      uint8_t* __restrict__ vc8,
-                                                      uint16_t* __restrict__ ksc,
-                                                      uint16_t* __restrict__ vsc,
-                                                      int dst_tok_base, int grp) {
-  const int h = blockIdx.x, t = threadIdx.x;
+// One group for kv head h, 256 threads: thread t owns token t/4, dims
+// 16*(t%4) .. +15, for K and for V.  Token row r of the group comes from the
+// tail when r < slot, else from source token src0 + r - slot (the tail rows
+// the reference would have copied it into hold the same fp16 values).
+__device__ __forceinline__ void commit_group_rows(const uint16_t* __restrict__ ktail,
+                                                  const uint16_t* __restrict__ vtail,
+                                                  const uint16_t* __restrict__ ksrc,
+                                                  const uint16_t* __restrict__ vsrc, int slot,
+                                                  int src0, uint8_t* __restrict__ kc8,
+                                                  uint8_t* __restrict__ vc8,
+                                                  uint16_t* __restrict__ ksc,
+                                                  uint16_t* __restrict__ vsc, int dst_tok_base,
+                                                  int grp, int h, int t) {
   const int tok = t >> 2, c = (t & 3) * 16;
-  const size_t src = ((size_t)tok * NKV + h) * D + c;
+  const bool from_tail = tok < slot;
+  const size_t row = from_tail ? (size_t)tok : (size_t)(src0 + tok - slot);
+  const size_t src = (row * NKV + h) * D + c;
+  const uint16_t* kp = (from_tail ? ktail : ksrc) + src;
+  const uint16_t* vp = (from_tail ? vtail : vsrc) + src;
   u32x4 kr[2], vr[2];
-  kr[0] = *(const u32x4*)(ktail + src);
-  kr[1] = *(const u32x4*)(ktail + src + 8);
-  vr[0] = *(const u32x4*)(vtail + src);
-  vr[1] = *(const u32x4*)(vtail + src + 8);
+  kr[0] = *(const u32x4*)kp;
+  kr[1] = *(const u32x4*)(kp + 8);
+  vr[0] = *(const u32x4*)vp;
+  vr[1] = *(const u32x4*)(vp + 8);
   float kf[16], vf[16];
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -75,6 +82,82 @@ __global__ __launch_bounds__(256) void k_commit_group(const uint16_t* __restrict
   const size_t dst = ((size_t)(dst_tok_base + tok) * NKV + h) * D + c;
   *(u32x4*)(kc8 + dst) = kb;
   *(u32x4*)(vc8 + dst) = vb;
+}
+
+// grid = 8 kv heads, block = 256: the group held in the tail
+__global__ __launch_bounds__(256) void k_commit_group(const uint16_t* __restrict__ ktail,
+                                                      const uint16_t* __restrict__ vtail,
+                                                      uint8_t* __restrict__ kc8,
+                                                      uint8_t* __restrict__ vc8,
+                                                      uint16_t* __restrict__ ksc,
+                                                      uint16_t* __restrict__ vsc,
+                                                      int dst_tok_base, int grp) {
+  commit_group_rows(ktail, vtail, nullptr, nullptr, G, 0, kc8, vc8, ksc, vsc, dst_tok_base, grp,
+                    blockIdx.x, threadIdx.x);
+}
+
+// ---------------------------------------------------------------- batched append
+// The placement loop of engine.cu:830-845 for S tokens arriving at tail
+// slot slot0, in two launches instead of two per group.  With cnt0 =
+// min(S, 64 - slot0): if slot0 + cnt0 = 64, group 0 is tail rows 0..slot0-1
+// plus source tokens 0..cnt0-1, and groups 1..nfull are source tokens
+// cnt0 + 64 (g-1) + r; the remaining cnt_last tokens stay in the tail.
+struct AppendShape {
+  int slot0, S, cnt0, commit0, nfull, s_last, cnt_last;
+};
+
+__host__ __device__ inline AppendShape append_shape(int slot0, int S) {
+  AppendShape a;
+  a.slot0 = slot0;
+  a.S = S;
+  a.cnt0 = S < G - slot0 ? S : G - slot0;
+  a.commit0 = slot0 + a.cnt0 == G;
+  a.nfull = a.commit0 ? (S - a.cnt0) / G : 0;
+  a.s_last = a.commit0 ? a.cnt0 + G * a.nfull : S;
+  a.cnt_last = S - a.s_last;
+  return a;
+}
+
+// grid = (1 + nfull, 8 kv heads), block = 256
+__global__ __launch_bounds__(256) void k_append_commit(const uint16_t* __restrict__ ktail,
+                                                       const uint16_t* __restrict__ vtail,
+                                                       const uint16_t* __restrict__ k,
+                                                       const uint16_t* __restrict__ v,
+                                                       uint8_t* __restrict__ kc8,
+                                                       uint8_t* __restrict__ vc8,
+                                                       uint16_t* __restrict__ ksc,
+                                                       uint16_t* __restrict__ vsc, AppendShape sh,
+                                                       int committed) {
+  const int g = blockIdx.x;
+  const int slot = g == 0 ? sh.slot0 : 0;
+  const int src0 = g == 0 ? 0 : sh.cnt0 + G * (g - 1);
+  commit_group_rows(ktail, vtail, k, v, slot, src0, kc8, vc8, ksc, vsc, committed + G * g,
+                    committed / G + g, blockIdx.y, threadIdx.x);
+}
+
+// The tail as the reference leaves it: row r holds the token the last op
+// that wrote row r put there.  grid = 64 rows, block = 64: lane -> (kv head
+// lane / 8, 16-byte chunk lane % 8) of K and of V.
+__global__ __launch_bounds__(64) void k_append_tail(uint16_t* __restrict__ ktail,
+                                                    uint16_t* __restrict__ vtail,
+                                                    const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v,
+                                                    AppendShape sh) {
+  const int r = blockIdx.x;
+  int src = -1;
+  if (!sh.commit0) {
+    if (r >= sh.slot0 && r < sh.slot0 + sh.S) src = r - sh.slot0;
+  } else if (r < sh.cnt_last) {
+    src = sh.s_last + r;
+  } else if (sh.nfull > 0) {
+    src = sh.cnt0 + G * (sh.nfull - 1) + r;
+  } else if (r >= sh.slot0) {
+    src = r - sh.slot0;
+  }
+  if (src < 0) return;
+  const size_t o = (size_t)threadIdx.x * 8;  // element offset inside the row (8 heads x 64)
+  *(u32x4*)(ktail + (size_t)r * NKV * D + o) = *(const u32x4*)(k + (size_t)src * NKV * D + o);
+  *(u32x4*)(vtail + (size_t)r * NKV * D + o) = *(const u32x4*)(v + (size_t)src * NKV * D + o);
 }
 
 // ---------------------------------------------------------------- H2O quant
@@ -174,6 +257,38 @@ extern "C" int cia_kv_commit_group(const uint16_t* ktail, const uint16_t* vtail,
   hipLaunchKernelGGL(k_commit_group, dim3(NKV), dim3(256), 0, (hipStream_t)stream, ktail, vtail,
                      kc8, vc8, ksc, vsc, dst_tok_base, grp);
   return launch_status();
+}
+
+// S tokens at positions past.. into the group-64 cache whose tail holds
+// tokens committed..past-1 (past - committed in [0, 64)); returns the new
+// committed count in *committed.  Internal entry of the layer driver.
+extern "C" __attribute__((visibility("hidden"))) int cia_kv_append_batched(
+    const uint16_t* k, const uint16_t* v, uint16_t* ktail, uint16_t* vtail, uint8_t* kc8,
+    uint8_t* vc8, uint16_t* ksc, uint16_t* vsc, int* committed, int S, int past, int maxT,
+    void* stream) {
+  CIA_REQUIRE(committed && k && v && ktail && vtail && kc8 && vc8 && ksc && vsc, CIA_ERR_NULL);
+  CIA_REQUIRE(aligned(k, 16) && aligned(v, 16) && aligned(ktail, 16) && aligned(vtail, 16) &&
+                  aligned(kc8, 16) && aligned(vc8, 16) && aligned(ksc, 2) && aligned(vsc, 2),
+              CIA_ERR_ALIGN);
+  const int c = *committed;
+  CIA_REQUIRE(S >= 0 && c >= 0 && c % G == 0, CIA_ERR_ARG);
+  CIA_REQUIRE(past >= c && past - c < G, CIA_ERR_STATE);
+  if (S == 0) return CIA_OK;
+  CIA_REQUIRE(past + S <= maxT, CIA_ERR_ARG);
+  const AppendShape sh = append_shape(past - c, S);
+  const int ncommit = sh.commit0 ? 1 + sh.nfull : 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (ncommit) {
+    hipLaunchKernelGGL(k_append_commit, dim3(ncommit, NKV), dim3(256), 0, s, ktail, vtail, k, v,
+                       kc8, vc8, ksc, vsc, sh, c);
+    const int st = launch_status();
+    if (st) return st;
+  }
+  hipLaunchKernelGGL(k_append_tail, dim3(G), dim3(64), 0, s, ktail, vtail, k, v, sh);
+  const int st = launch_status();
+  if (st) return st;
+  *committed = c + G * ncommit;
+  return CIA_OK;
 }
 
 extern "C" int cia_kv_quant_write(const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
