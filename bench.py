@@ -63,6 +63,8 @@ def main():
     ap.add_argument("--long-ctx", type=int, default=131072,
                     help="long-context decode leg: context tokens (0 = skip)")
     ap.add_argument("--long-steps", type=int, default=8)
+    ap.add_argument("--h2o-steps", type=int, default=4000,
+                    help="H2O decode steps after a 1024-token prompt (0 = skip)")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="MiB: first run a plain device copy of this size three times "
                          "(the reference dispatch that scales rocprofv3 byte counters)")
@@ -248,6 +250,9 @@ def main():
         torch.cuda.empty_cache()
         long_ctx = long_context_leg(a.long_ctx, nL, a.long_steps, dev, stream, log)
 
+    # ---- H2O leg: 2048-slot buffer, window 256, 1024-token prompt
+    h2o = h2o_leg(a.h2o_steps, dev, stream, log) if a.h2o_steps > 0 else None
+
     # ---- CPU baseline: the oracle on this host's cores, one layer at a time
     cpu = None
     if not a.no_cpu:
@@ -285,6 +290,7 @@ def main():
                                             "k_decode_finish": round(fin_us, 3)}},
         "prefill": prefill,
         "long_context": long_ctx,
+        "h2o": h2o,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
@@ -345,6 +351,63 @@ def long_context_leg(ctx, nL, steps, dev, stream, log):
         name = "matrix_core" if ns == 0 else f"split_{ns}"
         res[name] = {"us_per_token": round(us, 2), "gbps": round(gbps, 1)}
         log(f"long context {ctx}: {name}: {us:.1f} us/token, {gbps:.0f} GB/s")
+    return res
+
+
+def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
+    """H2O eviction decode on one layer: a C-slot per-token FP8 buffer,
+    window W, a P-token prompt, then `steps` single-token steps through the
+    decode loop (slot choice on the device, no host round trip), timed as a
+    whole; then 64 more steps with events around the placement launch and
+    the two attention launches."""
+    import ctypes
+    import torch
+    from cuda_inf_amd import _lib, workload
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd._lib import D, NH, NKV, call
+    extra = 64
+    total = P + steps + extra
+    L = AttnLayer(total + 64, budget=C, window=W, prompt_len=P, max_batch=P, device=dev)
+    g = workload.generator(7, dev)
+    q = workload.normal_f16((total, NH, D), g, dev)
+    k = workload.normal_f16((total, NKV, D), g, dev)
+    v = workload.normal_f16((total, NKV, D), g, dev)
+    out = torch.empty((total, NH, D), dtype=torch.float16, device=dev)
+    L.forward(q[:P], k[:P], v[:P], 0, out=out[:P], evicted=False)
+    torch.cuda.synchronize()
+    qrow, krow = NH * D * 2, NKV * D * 2
+
+    def loop(s0, n, events=None):
+        call("cia_decode_loop", ctypes.byref(L._s), 1, q.data_ptr() + s0 * qrow,
+             k.data_ptr() + s0 * krow, v.data_ptr() + s0 * krow, out.data_ptr() + s0 * qrow,
+             s0, n, 0.125, events, stream.cuda_stream)
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    loop(P, steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * extra)]
+    for e in evs:  # the hipEvent_t handles exist once recorded
+        e.record(stream)
+    torch.cuda.synchronize()
+    ptrs = (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs])
+    loop(P + steps, extra, ptrs)
+    torch.cuda.synchronize()
+    place = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) * 1e3 for i in range(extra))
+    attn = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) * 1e3 for i in range(extra))
+    # per step: FP8 K+V and fp16 scales of every live slot, its position
+    # and mass (read + write), q in, out written
+    step_bytes = C * (2 * NKV * D + 2 * NKV * 2 + 4 + 8) + 2 * NH * D * 2
+    res = {"slots": C, "window": W, "prompt": P, "steps": steps, "us_per_step": round(us, 2),
+           "gbps": round(step_bytes / (us * 1e-6) / 1e9, 1),
+           "place_us_median": round(place[extra // 2], 2),
+           "attention_us_median": round(attn[extra // 2], 2),
+           "evictions": steps + extra + P - C,
+           "policy": "device slot choice (cia_h2o_place), no host round trip"}
+    log(f"h2o C={C} W={W}: {us:.2f} us/step over {steps} steps; place {res['place_us_median']} us,"
+        f" attention {res['attention_us_median']} us (medians)")
     return res
 
 

@@ -39,6 +39,7 @@ SIGNATURES = {
     "cia_attn_decode": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, ctypes.c_int64, _P]),
     "cia_decode_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_kv_quant_write": (_I, [_P] * 7 + [_I, _P]),
+    "cia_h2o_place": (_I, [_P] * 10 + [_I, _I, _I, _I, _P]),
     "cia_attention_h2o": (_I, [_P] * 6 + [_I, _P, _P, _I, _I, _F, _P, _P]),
     "cia_mass_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_kv_append_plan": (_I, [_P, _I, _I, _P, _I, _P]),
@@ -111,5 +112,5 @@ class cia_layer(ctypes.Structure):
         ("nsplit", _I), ("pm", _P), ("pl", _P), ("po", _P), ("ws_decode", _P),
         ("budget", _I), ("window", _I),
         ("kf", _P), ("vf", _P), ("ks", _P), ("vs", _P), ("hattn", _P), ("d_slotpos", _P),
-        ("d_dst", _P), ("h_slotpos", _P), ("h_attn", _P), ("n_live", _I), ("ws_mass", _P),
+        ("d_dst", _P), ("n_live", _I), ("ws_mass", _P),
     ]

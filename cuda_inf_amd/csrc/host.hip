@@ -139,60 +139,34 @@ extern "C" int cia_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos, f
 // ---------------------------------------------------------------- layer driver
 namespace {
 
-__global__ void k_zero_picked(float* attn, const int32_t* dst, const int32_t* zero_flags, int S) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j < S && zero_flags[j]) attn[dst[j]] = 0.0f;
-}
-
+// engine.cu:803-828 with the slot choice on the device: place + quantise,
+// then attention with the mass update; no host round trip
 int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                uint16_t* out, int S, int past, float scale, int* evicted, void* stream) {
-  hipStream_t s = (hipStream_t)stream;
+                uint16_t* out, int S, int past, float scale, int* evicted, void* stream,
+                void* mid_event = nullptr) {
   const int C = L->budget;
   if (!L->kf || !L->vf || !L->ks || !L->vs || !L->hattn || !L->d_slotpos || !L->d_dst ||
-      !L->h_slotpos || !L->h_attn || !L->ws_mass)
+      !L->ws_mass)
     return CIA_ERR_NULL;
-  // the reference fetches attn_sum only when a slot must be evicted
-  // (engine.cu:813-814); the fetch is a blocking copy
-  const bool will_evict = L->n_live + S > C;
-  if (will_evict) {
-    int st = hip_check(hipMemcpyAsync(L->h_attn, L->hattn, sizeof(float) * C,
-                                      hipMemcpyDeviceToHost, s));
+  const int n0 = L->n_live;
+  int st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
+                         &L->n_live, C, L->window, S, past, stream);
+  if (st) return st;
+  if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
+    return st;
+  st = cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out, L->hattn,
+                         S, past, scale, L->ws_mass, stream);
+  if (st) return st;
+  // the last token evicted iff it found no free slot
+  if (evicted && n0 + S > C) {
+    int32_t slot = -1;
+    st = hip_check(hipMemcpyAsync(&slot, L->d_dst + (S - 1), sizeof(slot), hipMemcpyDeviceToHost,
+                                  (hipStream_t)stream));
     if (st) return st;
-    st = hip_check(hipStreamSynchronize(s));
-    if (st) return st;
+    if ((st = hip_check(hipStreamSynchronize((hipStream_t)stream)))) return st;
+    *evicted = slot;
   }
-  // dst and the zero flags travel in one H2D copy: d_dst[0..S), d_dst[S..2S)
-  static thread_local int32_t* hbuf = nullptr;
-  static thread_local int hcap = 0;
-  if (hcap < 2 * S) {
-    delete[] hbuf;
-    hbuf = new int32_t[2 * S];
-    hcap = 2 * S;
-  }
-  const int ev = cia_h2o_pick_slots(&L->n_live, C, L->window, L->h_slotpos, L->h_attn, S, past,
-                                    hbuf, hbuf + S);
-  if (ev < 0) return -ev;
-  if (evicted) *evicted = -1;
-  for (int j = 0; j < S && evicted; j++)
-    if (hbuf[S + j]) *evicted = hbuf[j];
-  int st = hip_check(hipMemcpyAsync(L->d_dst, hbuf, sizeof(int32_t) * 2 * S,
-                                    hipMemcpyHostToDevice, s));
-  if (st) return st;
-  st = hip_check(hipMemcpyAsync(L->d_slotpos, L->h_slotpos, sizeof(int32_t) * C,
-                                hipMemcpyHostToDevice, s));
-  if (st) return st;
-  // the host buffers are reused by the next call: wait for the copies
-  st = hip_check(hipStreamSynchronize(s));
-  if (st) return st;
-  if (ev > 0) {
-    hipLaunchKernelGGL(k_zero_picked, dim3((S + 255) / 256), dim3(256), 0, s, L->hattn, L->d_dst,
-                       L->d_dst + S, S);
-    if ((st = launch_status())) return st;
-  }
-  st = cia_kv_quant_write(k, v, L->kf, L->vf, L->ks, L->vs, L->d_dst, S, stream);
-  if (st) return st;
-  return cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out, L->hattn,
-                           S, past, scale, L->ws_mass, stream);
+  return CIA_OK;
 }
 
 // placement loop (engine.cu:830-845): copy into the tail, commit full
@@ -282,8 +256,6 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
                                int steps, float scale, void** events, void* stream) {
   if (!layers || !q || !k || !v || !out) return CIA_ERR_NULL;
   if (n_layers < 1 || steps < 0 || past < 0) return CIA_ERR_ARG;
-  for (int l = 0; l < n_layers; l++)
-    if (layers[l].budget > 0) return CIA_ERR_STATE;
   const size_t qrow = (size_t)CIA_NH * CIA_HEAD_DIM, krow = (size_t)CIA_NKV * CIA_HEAD_DIM;
   hipStream_t s = (hipStream_t)stream;
   for (int i = 0; i < steps; i++) {
@@ -292,6 +264,14 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
       cia_layer* L = &layers[l];
       const int pos = past + i;
       int st;
+      if (L->budget > 0) {
+        if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r], s)))) return st;
+        st = h2o_forward(L, q + r * qrow, k + r * krow, v + r * krow, out + r * qrow, 1, pos,
+                         scale, nullptr, stream, events ? events[3 * r + 1] : nullptr);
+        if (st) return st;
+        if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
+        continue;
+      }
       const bool fused = fused_append_ok(L, pos);
       if (!fused) {
         st = group64_append(L, k + r * krow, v + r * krow, 1, pos, stream);

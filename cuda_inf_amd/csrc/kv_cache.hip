@@ -1,9 +1,12 @@
 // kv_cache.hip -- the FP8 E4M3 KV writers of the cuda_inf attention path on
 // gfx950: tail append and group-64 commit (engine.cu:184-228), and the H2O
-// per-token slot quantiser (engine.cu:317-333).  All three are bit-exact:
-// amax is an order-free max, the scale is amax/448 + 1e-12 with an IEEE
-// division, the bytes are encoded from x / scale (fp32) and the stored scale
-// is fp16(scale).
+// per-token slot quantiser (engine.cu:317-333), with the H2O slot choice
+// (engine.cu:808-823) run on the device in front of it.  The writers are
+// bit-exact: amax is an order-free max, the scale is amax/448 + 1e-12 with
+// an IEEE division, the bytes are encoded from x / scale (fp32) and the
+// stored scale is fp16(scale).
+#include <algorithm>
+
 #include "common.h"
 
 namespace cia {
@@ -161,20 +164,20 @@ __global__ __launch_bounds__(64) void k_append_tail(uint16_t* __restrict__ ktail
 }
 
 // ---------------------------------------------------------------- H2O quant
-// grid = S * 8 (token, kv head), block = 64: lane d.
-__global__ __launch_bounds__(64) void k_quant_write(const uint16_t* __restrict__ k,
-                                                    const uint16_t* __restrict__ v,
-                                                    uint8_t* __restrict__ kf,
-                                                    uint8_t* __restrict__ vf,
-                                                    uint16_t* __restrict__ ks,
-                                                    uint16_t* __restrict__ vs,
-                                                    const int32_t* __restrict__ dst_slots) {
-  const int jh = blockIdx.x, j = jh / NKV, h = jh % NKV, d = threadIdx.x;
+// Token j, kv head h of k/v into slot `slot` of the H2O buffer; one wave,
+// lane d owns dimension d.  A slot < 0 (no slot could be chosen) writes
+// nothing.  Called with wave-uniform arguments.
+__device__ __forceinline__ void quant_write_row(const uint16_t* __restrict__ k,
+                                                const uint16_t* __restrict__ v,
+                                                uint8_t* __restrict__ kf, uint8_t* __restrict__ vf,
+                                                uint16_t* __restrict__ ks,
+                                                uint16_t* __restrict__ vs, int j, int h, int slot,
+                                                int d) {
+  if (slot < 0) return;
   const size_t src = ((size_t)j * NKV + h) * D + d;
   const float kv = h2f(k[src]), vv = h2f(v[src]);
   const float mk = wave_max_fast(__builtin_fabsf(kv)), mv = wave_max_fast(__builtin_fabsf(vv));
   const float sck = quant_scale(mk), scv = quant_scale(mv);
-  const int slot = dst_slots[j];
   // pack 4 neighbouring lanes' bytes into one dword store
   uint32_t kb = e4m3x2(kv / sck, 0.f) & 0xFFu, vb = e4m3x2(vv / scv, 0.f) & 0xFFu;
   uint32_t kw = kb << (8 * (d & 3)), vw = vb << (8 * (d & 3));
@@ -191,6 +194,124 @@ __global__ __launch_bounds__(64) void k_quant_write(const uint16_t* __restrict__
     ks[slot * NKV + h] = f2h(sck);
     vs[slot * NKV + h] = f2h(scv);
   }
+}
+
+// grid = S * 8 (token, kv head), block = 64: lane d.  With slot_pos, token j
+// writes only if slot_pos[slot] == past + j, i.e. no later token of the
+// batch took the same slot (the last write of the per-token order wins).
+__global__ __launch_bounds__(64) void k_quant_write(const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v,
+                                                    uint8_t* __restrict__ kf,
+                                                    uint8_t* __restrict__ vf,
+                                                    uint16_t* __restrict__ ks,
+                                                    uint16_t* __restrict__ vs,
+                                                    const int32_t* __restrict__ dst_slots,
+                                                    const int32_t* __restrict__ slot_pos,
+                                                    int past) {
+  const int jh = blockIdx.x, j = jh / NKV, h = jh % NKV;
+  const int slot = dst_slots[j];
+  if (slot_pos && slot >= 0 && slot_pos[slot] != past + j) return;
+  quant_write_row(k, v, kf, vf, ks, vs, j, h, slot, threadIdx.x);
+}
+
+// ---------------------------------------------------------------- H2O placement
+// The slot choice of engine.cu:808-823 on the device.  One block of
+// kPlaceThreads threads; thread i owns slots t with t % kPlaceThreads == i
+// and is the only thread that reads or writes attn[t] and slotpos[t], so
+// every value it reads is its own last write (no cross-thread visibility
+// is needed).  Token j < nfill takes slot n_live + j.  Each later token
+// takes the minimum (attn, slot) over slots with attn < 1e30 and
+// slotpos <= pos - W, else over all slots with attn < 1e30: the first
+// strict minimum of the reference's ascending scan, since -0 and +0 compare
+// equal there and are given one key here, and NaN never passes < 1e30.
+// A chosen slot is marked 1e30 until the end of the batch, then cleared
+// to 0 (the reference marks its host copy and clears the device value).
+// A slot filled earlier in the same batch can be chosen again; its filling
+// token is then not written (its bytes would be overwritten in the
+// reference's per-token order).  Up to kPlaceFuse tokens are also
+// quantised into their slots here.
+constexpr int kPlaceThreads = 1024;
+constexpr int kPlaceFuse = 16;
+constexpr float kPicked = 1e30f;
+
+__device__ __forceinline__ uint64_t place_key(float a, int t) {
+  uint32_t b = __float_as_uint(a == 0.0f ? 0.0f : a);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // float order as unsigned order
+  return ((uint64_t)b << 32) | (uint32_t)t;
+}
+
+__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return b < a ? b : a; }
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = min_u64(x, __shfl_xor(x, off));
+  return x;
+}
+
+__global__ __launch_bounds__(kPlaceThreads) void k_h2o_place(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint8_t* __restrict__ kf,
+    uint8_t* __restrict__ vf, uint16_t* __restrict__ ks, uint16_t* __restrict__ vs,
+    float* __restrict__ attn, int32_t* __restrict__ slotpos, int32_t* __restrict__ dst,
+    int n_live, int C, int W, int S, int past, int fuse) {
+  constexpr int kWaves = kPlaceThreads / 64;
+  __shared__ uint64_t red[2][2][kWaves];
+  __shared__ int slot_of[kPlaceFuse];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nfill = min(S, C - n_live);
+  for (int t = tid; t < C; t += kPlaceThreads)
+    if (t >= n_live && t < n_live + nfill) {
+      const int j = t - n_live;
+      slotpos[t] = past + j;
+      dst[j] = t;
+      if (fuse) slot_of[j] = t;
+    }
+  for (int j = nfill; j < S; j++) {
+    const int posj = past + j, lim = posj - W;
+    uint64_t kwin = ~0ull, kall = ~0ull;
+    for (int t = tid; t < C; t += kPlaceThreads) {
+      const float a = attn[t];
+      if (a < kPicked) {
+        const uint64_t key = place_key(a, t);
+        kall = min_u64(kall, key);
+        if (slotpos[t] <= lim) kwin = min_u64(kwin, key);
+      }
+    }
+    kwin = wave_min_u64(kwin);
+    kall = wave_min_u64(kall);
+    const int p = j & 1;  // alternate buffers: one barrier per token
+    if (lane == 0) {
+      red[p][0][wave] = kwin;
+      red[p][1][wave] = kall;
+    }
+    __syncthreads();
+    kwin = red[p][0][0];
+    kall = red[p][1][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; w++) {
+      kwin = min_u64(kwin, red[p][0][w]);
+      kall = min_u64(kall, red[p][1][w]);
+    }
+    const uint64_t kb = kwin != ~0ull ? kwin : kall;
+    const int best = kb != ~0ull ? (int)(uint32_t)kb : -1;
+    if (best >= 0 && best % kPlaceThreads == tid) {
+      attn[best] = kPicked;
+      slotpos[best] = posj;
+    }
+    if (tid == 0) {
+      dst[j] = best;
+      if (fuse) {
+        slot_of[j] = best;
+        if (best >= n_live && best < n_live + nfill) slot_of[best - n_live] = -1;
+      }
+    }
+  }
+  if (nfill < S)
+    for (int t = tid; t < C; t += kPlaceThreads)
+      if (attn[t] == kPicked) attn[t] = 0.0f;  // a reused slot starts fresh
+  if (!fuse) return;
+  __syncthreads();
+  for (int jh = wave; jh < S * NKV; jh += kWaves)
+    quant_write_row(k, v, kf, vf, ks, vs, jh / NKV, jh % NKV, slot_of[jh / NKV], lane);
 }
 
 // ---------------------------------------------------------------- codec check
@@ -299,6 +420,36 @@ extern "C" int cia_kv_quant_write(const uint16_t* k, const uint16_t* v, uint8_t*
   CIA_REQUIRE(k && v && kf && vf && ks && vs && dst_slots, CIA_ERR_NULL);
   CIA_REQUIRE(aligned(kf, 4) && aligned(vf, 4) && aligned(k, 2) && aligned(v, 2), CIA_ERR_ALIGN);
   hipLaunchKernelGGL(k_quant_write, dim3(S * NKV), dim3(64), 0, (hipStream_t)stream, k, v, kf, vf,
-                     ks, vs, dst_slots);
+                     ks, vs, dst_slots, (const int32_t*)nullptr, 0);
   return launch_status();
+}
+
+extern "C" int cia_h2o_place(const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
+                             uint16_t* ks, uint16_t* vs, float* attn_sum, int32_t* slot_pos,
+                             int32_t* dst_slots, int* n_live, int C, int W, int S, int past,
+                             void* stream) {
+  CIA_REQUIRE(n_live, CIA_ERR_NULL);
+  CIA_REQUIRE(S >= 0 && past >= 0 && C >= 1 && W >= 0 && *n_live >= 0 && *n_live <= C,
+              CIA_ERR_ARG);
+  if (S == 0) return CIA_OK;
+  CIA_REQUIRE(k && v && kf && vf && ks && vs && attn_sum && slot_pos && dst_slots, CIA_ERR_NULL);
+  CIA_REQUIRE(aligned(kf, 4) && aligned(vf, 4) && aligned(k, 2) && aligned(v, 2) &&
+                  aligned(attn_sum, 4) && aligned(slot_pos, 4) && aligned(dst_slots, 4),
+              CIA_ERR_ALIGN);
+  const int nfill = std::min(S, C - *n_live);
+  // more evictions than slots: the reference's scan runs out of slots < 1e30
+  if (S - nfill > C) return CIA_ERR_NOSLOT;
+  const int fuse = S <= kPlaceFuse;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_h2o_place, dim3(1), dim3(kPlaceThreads), 0, s, k, v, kf, vf, ks, vs,
+                     attn_sum, slot_pos, dst_slots, *n_live, C, W, S, past, fuse);
+  int st = launch_status();
+  if (st) return st;
+  if (!fuse) {
+    hipLaunchKernelGGL(k_quant_write, dim3(S * NKV), dim3(64), 0, s, k, v, kf, vf, ks, vs,
+                       dst_slots, (const int32_t*)slot_pos, past);
+    if ((st = launch_status())) return st;
+  }
+  *n_live += nfill;
+  return CIA_OK;
 }

@@ -8,6 +8,8 @@ raise ``CiaError``; there is no CPU fallback.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -127,6 +129,22 @@ def kv_quant_write(k, v, kf, vf, ks, vs, dst_slots, S: int) -> None:
          _dev(kf, "kf", (torch.uint8,)), _dev(vf, "vf", (torch.uint8,)),
          _dev(ks, "ks", _F16), _dev(vs, "vs", _F16),
          _dev(dst_slots, "dst_slots", (torch.int32,), S), S, _stream())
+
+
+def h2o_place(k, v, kf, vf, ks, vs, attn_sum, slot_pos, dst_slots, n_live: int, C: int, W: int,
+              S: int, past: int) -> int:
+    """engine.cu:808-826 on the device: slot choice + per-token quantisation.
+
+    Updates attn_sum, slot_pos, dst_slots in place; returns the new n_live."""
+    nl = ctypes.c_int(n_live)
+    call("cia_h2o_place", _dev(k, "k", _F16, S * NKV * D), _dev(v, "v", _F16, S * NKV * D),
+         _dev(kf, "kf", (torch.uint8,), C * NKV * D), _dev(vf, "vf", (torch.uint8,), C * NKV * D),
+         _dev(ks, "ks", _F16, C * NKV), _dev(vs, "vs", _F16, C * NKV),
+         _dev(attn_sum, "attn_sum", (torch.float32,), C),
+         _dev(slot_pos, "slot_pos", (torch.int32,), C),
+         _dev(dst_slots, "dst_slots", (torch.int32,), S), ctypes.byref(nl), C, W, S, past,
+         _stream())
+    return nl.value
 
 
 def mass_workspace_bytes(S: int) -> int:

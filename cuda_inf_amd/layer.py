@@ -100,13 +100,10 @@ class AttnLayer:
             self.vs = torch.zeros((C, NKV), dtype=f16, device=dev)
             self.hattn = torch.zeros(C, dtype=f32, device=dev)
             self.d_slotpos = torch.full((C,), -1, dtype=i32, device=dev)
-            self.d_dst = torch.zeros(2 * max_batch, dtype=i32, device=dev)
-            self.h_slotpos = torch.full((C,), -1, dtype=i32).pin_memory()
-            self.h_attn = torch.zeros(C, dtype=f32).pin_memory()
+            self.d_dst = torch.zeros(max_batch, dtype=i32, device=dev)
             self.ws_mass = torch.zeros(max(mass_workspace_bytes(max_batch), 8), dtype=u8, device=dev)
             s.budget, s.window = budget, window
-            for name in ("kf", "vf", "ks", "vs", "hattn", "d_slotpos", "d_dst", "h_slotpos",
-                         "h_attn", "ws_mass"):
+            for name in ("kf", "vf", "ks", "vs", "hattn", "d_slotpos", "d_dst", "ws_mass"):
                 setattr(s, name, getattr(self, name).data_ptr())
             s.n_live = 0
         self.max_batch = max_batch
@@ -120,10 +117,12 @@ class AttnLayer:
     def n_live(self) -> int:
         return self._s.n_live
 
-    def forward(self, q, k, v, past: int, out=None, scale: float = 0.125):
+    def forward(self, q, k, v, past: int, out=None, scale: float = 0.125, evicted: bool = True):
         """Append k, v [S,8,64] at positions past.. and attend q [S,32,64].
 
-        Returns (out [S,32,64] fp16, evicted slot of the last token or -1)."""
+        Returns (out [S,32,64] fp16, evicted slot of the last token or -1).
+        On an H2O layer the evicted slot is read back from the device, which
+        waits for the stream; ``evicted=False`` skips that (returns None)."""
         S = k.shape[0]
         if self.budget and S > self.max_batch:
             raise ValueError(f"S={S} exceeds max_batch={self.max_batch}")
@@ -134,6 +133,6 @@ class AttnLayer:
             out = torch.empty((S, NH, D), dtype=torch.float16, device=self.device)
         ev = ctypes.c_int(-1)
         call("cia_layer_forward", ctypes.byref(self._s), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-             out.data_ptr(), S, past, float(scale), ctypes.byref(ev),
+             out.data_ptr(), S, past, float(scale), ctypes.byref(ev) if evicted else None,
              torch.cuda.current_stream().cuda_stream)
-        return out, ev.value
+        return out, (ev.value if evicted else None)

@@ -158,6 +158,28 @@ int cia_kv_quant_write(const uint16_t* k, const uint16_t* v, uint8_t* kf,
                        uint8_t* vf, uint16_t* ks, uint16_t* vs,
                        const int32_t* dst_slots, int S, void* stream);
 
+/* The H2O slot choice of engine.cu:808-825 on the device, followed by
+ * kv_quant_write (engine.cu:317-333; launch engine.cu:826): replaces the
+ * host loop, its attn_sum fetch, the per-eviction cudaMemset and the
+ * dst / slot_pos uploads, so nothing blocks.  Same rule as
+ * cia_h2o_pick_slots, same results: token j (position past + j) takes slot
+ * *n_live + j while slots are free; after that the slot of least attn_sum
+ * (lowest index on ties) among slots with slot_pos <= past + j - W and
+ * attn_sum < 1e30, else among all slots with attn_sum < 1e30.  A chosen
+ * slot is not chosen again in the call; its attn_sum is cleared to 0 and
+ * its slot_pos set to past + j.  slot_pos[C], attn_sum[C] (device) are
+ * updated, dst_slots[S] (device) receives each token's slot (-1, and the
+ * token is not written, only when every candidate's attn_sum is NaN).
+ * When a token takes a slot that an earlier token of the call filled, the
+ * slot holds the later token, as after the reference's per-token writes.
+ * *n_live (host) advances by the tokens that took free slots.  Returns
+ * CIA_ERR_NOSLOT, before any device work, when the call would evict more
+ * than C slots.  W >= 0, 0 <= *n_live <= C. */
+int cia_h2o_place(const uint16_t* k, const uint16_t* v, uint8_t* kf,
+                  uint8_t* vf, uint16_t* ks, uint16_t* vs, float* attn_sum,
+                  int32_t* slot_pos, int32_t* dst_slots, int* n_live, int C,
+                  int W, int S, int past, void* stream);
+
 /* attention_h2o (engine.cu:337-384; launch engine.cu:827-828).
  * Attention of S queries over the n_live slots whose slot_pos <= qpos;
  * out [S][32][64] fp16.  attn_sum[t] (device f32, required as in the
@@ -215,8 +237,9 @@ int cia_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos,
 /* ------------------------------------------------------------------ */
 
 /* Device buffers of one attention layer (caller-owned, engine.cu:596-613)
- * plus the host state the reference keeps beside them (committed[l],
- * n_live[l], slotpos_h[l]). */
+ * plus the host counters the reference keeps beside them (committed[l],
+ * n_live[l]); its host slot positions (slotpos_h[l]) live on the device
+ * only, in d_slotpos. */
 typedef struct cia_layer {
   /* group-64 cache */
   uint8_t* kc8; uint8_t* vc8; uint16_t* ksc; uint16_t* vsc;
@@ -231,10 +254,8 @@ typedef struct cia_layer {
   int budget, window;
   uint8_t* kf; uint8_t* vf; uint16_t* ks; uint16_t* vs;
   float* hattn;          /* device attn_sum [budget] */
-  int32_t* d_slotpos;    /* device [budget] */
+  int32_t* d_slotpos;    /* device [budget], slot positions (-1: free) */
   int32_t* d_dst;        /* device [max tokens per call] */
-  int32_t* h_slotpos;    /* host [budget] */
-  float* h_attn;         /* host scratch [budget] */
   int n_live;
   void* ws_mass;         /* cia_mass_workspace_bytes(max tokens per call) */
 } cia_layer;
@@ -242,9 +263,11 @@ typedef struct cia_layer {
 /* Append S fresh tokens (k, v: device fp16 [S][8][64]) then attend q
  * (device fp16 [S][32][64]) into out, exactly as engine.cu:802-857:
  * H2O when budget > 0, else append + (S == 1 ? flash-decoding : fused).
- * H2O mode performs the reference's blocking copies (engine.cu:814,
- * 824-825) on `stream`.  On return *evicted (may be NULL) holds the slot
- * evicted for the last token, or -1. */
+ * H2O mode chooses slots on the device (cia_h2o_place) where the reference
+ * blocks on copies (engine.cu:814, 824-825).  evicted (may be NULL): on
+ * return *evicted holds the slot evicted for the last token, or -1; when
+ * that token evicted, reading the slot back synchronises `stream`, so pass
+ * NULL to keep the call asynchronous. */
 int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t* k,
                       const uint16_t* v, uint16_t* out, int S, int past,
                       float scale, int* evicted, void* stream);
@@ -264,7 +287,10 @@ int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t* v,
  * recorded before the layer's attention launches (after any separate append
  * launches), events[3r+1] between the first attention launch and the second
  * (after the only one when there is one) and events[3r+2] after the last:
- * per-kernel timing on the stream the kernels run on.  Group-64 layers only. */
+ * per-kernel timing on the stream the kernels run on.  On an H2O layer
+ * (budget > 0) events[3r] precedes the slot placement, events[3r+1]
+ * follows it and events[3r+2] follows the attention; no evicted slot is
+ * read back, so the loop never waits on the stream. */
 int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
                     const uint16_t* k, const uint16_t* v, uint16_t* out,
                     int past, int steps, float scale, void** events,

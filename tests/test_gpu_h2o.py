@@ -52,7 +52,7 @@ def test_h2o_small_stepwise(orc, cia, dev):
             i = int(np.argmax(got != ref.attn))
             raise AssertionError(f"step {j}: attn_sum differs at slot {i}: "
                                  f"{got[i]!r} vs {ref.attn[i]!r}")
-        assert np.array_equal(L.h_slotpos.numpy(), ref.slotpos)
+        assert np.array_equal(L.d_slotpos.cpu().numpy(), ref.slotpos)
         assert_close_f16(_u16(out), r32, what=f"step {j}")
     assert n_ev == N + P - C
 
@@ -84,4 +84,121 @@ def test_h2o_eviction_golden(cia, dev):
         j = int(np.argmax(evicted != ref))
         raise AssertionError(f"first divergence at step {j}: gpu {evicted[j]} oracle {ref[j]}")
     assert np.array_equal(L.hattn.cpu().numpy().view(np.uint32), g["attn_sum"].view(np.uint32))
-    assert np.array_equal(L.h_slotpos.numpy(), g["slotpos"])
+    assert np.array_equal(L.d_slotpos.cpu().numpy(), g["slotpos"])
+
+
+# (C, W, n_live, S, past, attn kind): fill only, fill then evict, the window
+# empty (fallback scan), more than one slot per thread, signed zeros and NaN
+# masses, an unfused batch of evictions
+PLACE_CASES = [
+    (64, 8, 0, 5, 0, "ties"),
+    (64, 8, 60, 10, 200, "ties"),
+    (64, 1000, 64, 3, 100, "ties"),
+    (3000, 256, 3000, 40, 5000, "ties"),
+    (3000, 256, 2990, 16, 5000, "zeros"),
+    (256, 16, 256, 7, 400, "nan"),
+    (256, 32, 200, 150, 300, "ties"),
+    (2048, 256, 2048, 1, 9000, "randn"),
+]
+
+
+@pytest.mark.parametrize("C,W,n_live,S,past,kind", PLACE_CASES)
+def test_h2o_place_matches_host_rule(orc, cia, dev, C, W, n_live, S, past, kind):
+    """cia_h2o_place against the oracle's restatement of engine.cu:808-826:
+    slots, slot positions, attention masses and quantised bytes bit-exact."""
+    from cuda_inf_amd import kernels as K
+    rng = np.random.default_rng(C * 7 + S)
+    if kind == "randn":
+        attn = np.abs(rng.standard_normal(C)).astype(np.float32)
+    else:
+        attn = rng.choice(np.array([0.0, 0.25, 0.5, 1.0], np.float32), C)
+    if kind == "zeros":
+        attn[rng.random(C) < 0.5] = -0.0
+    if kind == "nan":
+        attn[rng.random(C) < 0.3] = np.nan
+    attn[n_live:] = 0.0
+    slotpos = np.full(C, -1, np.int32)
+    slotpos[:n_live] = rng.integers(0, max(past, 1), n_live)
+    k = torch.randn((S, 8, 64), dtype=torch.float64,
+                    generator=torch.Generator().manual_seed(S)).to(torch.float16)
+    v = torch.randn((S, 8, 64), dtype=torch.float64,
+                    generator=torch.Generator().manual_seed(S + 1)).to(torch.float16)
+    # oracle: the host rule on copies, the device clears picked slots
+    r_slot, r_attn = slotpos.copy(), attn.copy()
+    r_nl, r_dst, r_zero, r_ev = orc.h2o_pick_slots(n_live, C, W, r_slot, r_attn.copy(), S, past)
+    assert r_ev >= 0
+    r_attn[r_dst[r_zero == 1]] = 0.0
+    rkf = np.zeros((C, 8, 64), np.uint8)
+    rvf = np.zeros_like(rkf)
+    rks = np.zeros((C, 8), np.uint16)
+    rvs = np.zeros_like(rks)
+    orc.kv_quant_write(_u16(k), _u16(v), rkf, rvf, rks, rvs, r_dst)
+    # device
+    d_attn = torch.from_numpy(attn.copy()).to(dev)
+    d_slot = torch.from_numpy(slotpos.copy()).to(dev)
+    d_dst = torch.full((S,), -7, dtype=torch.int32, device=dev)
+    kf = torch.zeros((C, 8, 64), dtype=torch.uint8, device=dev)
+    vf = torch.zeros_like(kf)
+    ks = torch.zeros((C, 8), dtype=torch.float16, device=dev)
+    vs = torch.zeros_like(ks)
+    print(f"h2o_place C={C} W={W} n_live={n_live} S={S} past={past} {kind}", flush=True)
+    nl = K.h2o_place(k.to(dev), v.to(dev), kf, vf, ks, vs, d_attn, d_slot, d_dst, n_live, C, W,
+                     S, past)
+    torch.cuda.synchronize()
+    assert nl == r_nl
+    assert np.array_equal(d_dst.cpu().numpy(), r_dst)
+    assert np.array_equal(d_slot.cpu().numpy(), r_slot)
+    assert np.array_equal(d_attn.cpu().numpy().view(np.uint32), r_attn.view(np.uint32))
+    assert np.array_equal(kf.cpu().numpy(), rkf)
+    assert np.array_equal(vf.cpu().numpy(), rvf)
+    assert np.array_equal(_u16(ks), rks)
+    assert np.array_equal(_u16(vs), rvs)
+
+
+def test_h2o_place_rejects_overflow(cia, dev):
+    """More evictions in one call than slots: CIA_ERR_NOSLOT before any launch."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd._lib import CiaError
+    C, S = 8, 20
+    z = lambda *s, dt=torch.uint8: torch.zeros(s, dtype=dt, device=dev)
+    attn = z(C, dt=torch.float32)
+    with pytest.raises(CiaError, match="NOSLOT"):
+        K.h2o_place(z(S, 8, 64, dt=torch.float16), z(S, 8, 64, dt=torch.float16), z(C, 8, 64),
+                    z(C, 8, 64), z(C, 8, dt=torch.float16), z(C, 8, dt=torch.float16), attn,
+                    z(C, dt=torch.int32), z(S, dt=torch.int32), 4, C, 2, S, 0)
+    assert float(attn.abs().sum()) == 0.0
+
+
+def test_h2o_decode_loop_matches_oracle(orc, cia, dev):
+    """The C decode loop over an H2O layer (no readback between steps):
+    C=128, W=16, 64-token prompt, 250 steps in three calls with other work
+    queued between them; every output, the final masses and positions
+    against the oracle."""
+    import ctypes
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    from cuda_inf_amd._lib import call
+    C, W, P, N = 128, 16, 64, 250
+    q, k, v = qkv(P + N, seed=33, device="cpu", prep=False)
+    qn, kn, vn = _u16(q), _u16(k), _u16(v)
+    L = AttnLayer(P + N + 4, budget=C, window=W, prompt_len=P, max_batch=P, device=dev)
+    ref = orc.H2OCache(C, W)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = torch.zeros((P + N, 32, 64), dtype=torch.float16, device=dev)
+    L.forward(qd[:P], kd[:P], vd[:P], 0, out=out[:P], evicted=False)
+    ref.step(qn[:P], kn[:P], vn[:P], 0)
+    s = torch.cuda.current_stream()
+    junk = torch.randn(1 << 20, device=dev)
+    for s0, n in ((P, 100), (P + 100, 1), (P + 101, N - 101)):
+        call("cia_decode_loop", ctypes.byref(L._s), 1, qd[s0].data_ptr(), kd[s0].data_ptr(),
+             vd[s0].data_ptr(), out[s0].data_ptr(), s0, n, 0.125, None, s.cuda_stream)
+        junk = junk * 1.0001 + 1.0  # eager work between the calls
+    torch.cuda.synchronize()
+    got = _u16(out)
+    for j in range(N):
+        pos = P + j
+        _, r16, r32 = ref.step(qn[pos:pos + 1], kn[pos:pos + 1], vn[pos:pos + 1], pos)
+        assert_close_f16(got[pos:pos + 1], r32, what=f"step {j}")
+    assert L.n_live == C
+    assert np.array_equal(L.hattn.cpu().numpy().view(np.uint32), ref.attn.view(np.uint32))
+    assert np.array_equal(L.d_slotpos.cpu().numpy(), ref.slotpos)
