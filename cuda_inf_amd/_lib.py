@@ -40,7 +40,8 @@ SIGNATURES = {
     "cia_decode_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_kv_quant_write": (_I, [_P] * 7 + [_I, _P]),
     "cia_h2o_place": (_I, [_P] * 10 + [_I, _I, _I, _I, _P]),
-    "cia_attention_h2o": (_I, [_P] * 6 + [_I, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_attention_h2o": (_I, [_P] * 6 + [_I, _P, _P, _I, _I, _F, _P, ctypes.c_int64, _P]),
+    "cia_h2o_workspace_bytes": (ctypes.c_int64, [_I, _I]),
     "cia_mass_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_kv_append_plan": (_I, [_P, _I, _I, _P, _I, _P]),
     "cia_h2o_clamp": (None, [_P, _P, _I, _I]),

@@ -155,7 +155,7 @@ int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16
   if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
     return st;
   st = cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out, L->hattn,
-                         S, past, scale, L->ws_mass, stream);
+                         S, past, scale, L->ws_mass, cia_h2o_workspace_bytes(S, C), stream);
   if (st) return st;
   // the last token evicted iff it found no free slot
   if (evicted && n0 + S > C) {

@@ -1,11 +1,12 @@
-// mass.hip -- attention_h2o (engine.cu:337-384) and the attn_sum option of
-// attention_fused (engine.cu:291-307) on gfx950.
+// mass.hip -- the attn_sum option of attention_fused (engine.cu:291-307) on
+// gfx950: the attention mass of every (query, head) added per key of the
+// group-64 cache.
 //
 // The reference adds every (query, head) probability into attn_sum with
-// atomicAdd in an undefined order and with an approximate __expf, so the
-// H2O eviction order it produces is not reproducible.  Here the mass is
-// computed with a fixed rule that gives identical bits on any IEEE-754
-// machine (the CPU restatement follows the same rule):
+// atomicAdd in an undefined order and with an approximate __expf.  Here the
+// mass is computed with the fixed rule of the H2O path, which gives
+// identical bits on any IEEE-754 machine (the CPU restatement follows the
+// same rule):
 //   s(t) = fma chain over d = 0..63 of q[d]*k(t)[d] from 0, times scale
 //   m    = max s over eligible keys
 //   e(t) = exp_det(s(t) - m)          (0 for ineligible keys)
@@ -22,37 +23,6 @@
 #include "common.h"
 
 namespace cia {
-
-// H2O slot buffer: per-slot FP8 with one fp16 scale per (slot, kv head);
-// slot t is visible to a query at qpos when slot_pos[t] <= qpos.
-struct SlotSrc {
-  const uint8_t* kf;
-  const uint8_t* vf;
-  const uint16_t* ks;
-  const uint16_t* vs;
-  const int32_t* slot_pos;
-  int n_live;
-  __device__ int count(int) const { return n_live; }
-  __device__ bool ok(int t, int qpos) const { return slot_pos[t] <= qpos; }
-  __device__ void key(int t, int kvh, float* x) const { row(kf, ks, t, kvh, x); }
-  __device__ void val(int t, int kvh, float* x) const { row(vf, vs, t, kvh, x); }
-  __device__ static void row(const uint8_t* c8, const uint16_t* sc, int t, int kvh, float* x) {
-    const u32x4* p = (const u32x4*)(c8 + ((size_t)t * NKV + kvh) * D);
-    const float s = h2f(sc[t * NKV + kvh]);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const u32x4 b = p[c];
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-        f32x2 lo = e4m3x2_to_f32<false>(b[w]), hi = e4m3x2_to_f32<true>(b[w]);
-        x[16 * c + 4 * w + 0] = lo[0] * s;
-        x[16 * c + 4 * w + 1] = lo[1] * s;
-        x[16 * c + 4 * w + 2] = hi[0] * s;
-        x[16 * c + 4 * w + 3] = hi[1] * s;
-      }
-    }
-  }
-};
 
 // group-64 cache: keys 0..qpos are visible; FP8 below `committed`
 struct Group64Src {
@@ -114,14 +84,11 @@ __device__ __forceinline__ float dot_chain(const float* q, const float* k) {
 }
 
 // Per (query i, kv head): wave w handles query head 4*kvh+w.  Writes
-// stats[(i*32+h)*2] = m, [..+1] = 1/l and, for H2O, the attention output.
-// block = 256, grid = (S, 8).
-template <class Src, bool kOut>
+// stats[(i*32+h)*2] = m, [..+1] = 1/l.  block = 256, grid = (S, 8).
+template <class Src>
 __global__ __launch_bounds__(256) void k_mass_stats(const uint16_t* __restrict__ q, Src src,
                                                     int past, float scale,
-                                                    float* __restrict__ stats,
-                                                    uint16_t* __restrict__ out) {
-  __shared__ float red[kOut ? 4 * 64 * 65 : 1];
+                                                    float* __restrict__ stats) {
   const int i = blockIdx.x, kvh = blockIdx.y;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = kvh * GQA + w, qpos = past + i;
@@ -137,38 +104,16 @@ __global__ __launch_bounds__(256) void k_mass_stats(const uint16_t* __restrict__
   }
   mx = wave_max(mx);
   float acc = 0.0f;
-  float o[kOut ? D : 1];
-  if constexpr (kOut) {
-#pragma unroll
-    for (int d = 0; d < D; d++) o[d] = 0.f;
-  }
   for (int t = lane; t < n; t += 64) {
     if (!src.ok(t, qpos)) continue;  // e = 0 adds nothing
     float kx[D];
     src.key(t, kvh, kx);
-    const float e = exp_det(dot_chain(qr, kx) * scale - mx);
-    acc = acc + e;
-    if constexpr (kOut) {
-      float vx[D];
-      src.val(t, kvh, vx);
-#pragma unroll
-      for (int d = 0; d < D; d++) o[d] = __builtin_fmaf(e, vx[d], o[d]);
-    }
+    acc = acc + exp_det(dot_chain(qr, kx) * scale - mx);
   }
   const float l = wave_sum(acc);  // the butterfly of the rule
-  const float inv = 1.0f / l;
   if (lane == 0) {
     stats[((size_t)i * NH + h) * 2] = mx;
-    stats[((size_t)i * NH + h) * 2 + 1] = inv;
-  }
-  if constexpr (kOut) {
-    float* r = red + w * 64 * 65;
-#pragma unroll
-    for (int d = 0; d < D; d++) r[lane * 65 + d] = o[d];
-    __syncthreads();
-    float sum = 0.f;
-    for (int j = 0; j < 64; j++) sum += r[j * 65 + lane];
-    out[((size_t)i * NH + h) * D + lane] = f2h(sum * inv);
+    stats[((size_t)i * NH + h) * 2 + 1] = 1.0f / l;
   }
 }
 
@@ -210,29 +155,6 @@ extern "C" int64_t cia_mass_workspace_bytes(int S) {
   return S < 0 ? 0 : (int64_t)S * NH * 2 * (int64_t)sizeof(float);
 }
 
-extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uint8_t* vf,
-                                 const uint16_t* ks, const uint16_t* vs,
-                                 const int32_t* slot_pos, int n_live, uint16_t* out,
-                                 float* attn_sum, int S, int past, float scale, void* ws,
-                                 void* stream) {
-  CIA_REQUIRE(S >= 0 && past >= 0 && n_live >= 0, CIA_ERR_ARG);
-  if (S == 0) return CIA_OK;
-  CIA_REQUIRE(q && kf && vf && ks && vs && slot_pos && out && attn_sum && ws, CIA_ERR_NULL);
-  CIA_REQUIRE(n_live >= 1, CIA_ERR_ARG);
-  CIA_REQUIRE(aligned(q, 16) && aligned(kf, 16) && aligned(vf, 16) && aligned(ws, 8) &&
-                  aligned(ks, 2) && aligned(vs, 2),
-              CIA_ERR_ALIGN);
-  SlotSrc src{kf, vf, ks, vs, slot_pos, n_live};
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((k_mass_stats<SlotSrc, true>), dim3(S, NKV), dim3(256), 0, s, q, src, past,
-                     scale, (float*)ws, out);
-  int st = launch_status();
-  if (st) return st;
-  hipLaunchKernelGGL((k_mass_accum<SlotSrc>), dim3((n_live + 63) / 64), dim3(64), 0, s, q, src, S,
-                     past, scale, (const float*)ws, attn_sum, n_live);
-  return launch_status();
-}
-
 // attn_sum of attention_fused over the group-64 cache (called after the
 // output kernel by cia_attention_fused).
 extern "C" __attribute__((visibility("hidden"))) int cia_mass_group64(const uint16_t* q, const uint8_t* kc8, const uint16_t* ksc,
@@ -242,8 +164,8 @@ extern "C" __attribute__((visibility("hidden"))) int cia_mass_group64(const uint
   CIA_REQUIRE(aligned(ws, 8), CIA_ERR_ALIGN);
   Group64Src src{kc8, ksc, ktail, committed};
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((k_mass_stats<Group64Src, false>), dim3(S, NKV), dim3(256), 0, s, q, src,
-                     past, scale, (float*)ws, (uint16_t*)nullptr);
+  hipLaunchKernelGGL((k_mass_stats<Group64Src>), dim3(S, NKV), dim3(256), 0, s, q, src, past,
+                     scale, (float*)ws);
   int st = launch_status();
   if (st) return st;
   const int nkeys = past + S;

@@ -151,12 +151,18 @@ def mass_workspace_bytes(S: int) -> int:
     return int(_lib.lib().cia_mass_workspace_bytes(S))
 
 
+def h2o_workspace_bytes(S: int, C: int) -> int:
+    return int(_lib.lib().cia_h2o_workspace_bytes(S, C))
+
+
 def attention_h2o(q, kf, vf, ks, vs, slot_pos, n_live: int, out, attn_sum, S: int, past: int,
                   scale: float, ws) -> None:
-    """engine.cu:337-384 with the deterministic attention-mass rule."""
+    """engine.cu:337-384 with the deterministic attention-mass rule; ws is a
+    uint8 device tensor of at least h2o_workspace_bytes(S, n_live) bytes."""
     call("cia_attention_h2o", _dev(q, "q", _F16, S * NH * D),
          _dev(kf, "kf", (torch.uint8,), n_live * NKV * D), _dev(vf, "vf", (torch.uint8,), n_live * NKV * D),
          _dev(ks, "ks", _F16, n_live * NKV), _dev(vs, "vs", _F16, n_live * NKV),
          _dev(slot_pos, "slot_pos", (torch.int32,), n_live), n_live,
          _dev(out, "out", _F16, S * NH * D), _dev(attn_sum, "attn_sum", (torch.float32,), n_live),
-         S, past, float(scale), _dev(ws, "ws", None, mass_workspace_bytes(S)), _stream())
+         S, past, float(scale), _dev(ws, "ws", (torch.uint8,), h2o_workspace_bytes(S, n_live)),
+         ws.numel(), _stream())

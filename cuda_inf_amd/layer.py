@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import D, KVGROUP, NH, NKV, NSPLIT_DEFAULT, call, cia_append_op, cia_layer
-from .kernels import decode_workspace_bytes, mass_workspace_bytes
+from .kernels import decode_workspace_bytes, h2o_workspace_bytes
 
 
 # ------------------------------------------------------------ host policy
@@ -101,7 +101,7 @@ class AttnLayer:
             self.hattn = torch.zeros(C, dtype=f32, device=dev)
             self.d_slotpos = torch.full((C,), -1, dtype=i32, device=dev)
             self.d_dst = torch.zeros(max_batch, dtype=i32, device=dev)
-            self.ws_mass = torch.zeros(max(mass_workspace_bytes(max_batch), 8), dtype=u8, device=dev)
+            self.ws_mass = torch.zeros(h2o_workspace_bytes(max_batch, C), dtype=u8, device=dev)
             s.budget, s.window = budget, window
             for name in ("kf", "vf", "ks", "vs", "hattn", "d_slotpos", "d_dst", "ws_mass"):
                 setattr(s, name, getattr(self, name).data_ptr())

@@ -188,12 +188,16 @@ int cia_h2o_place(const uint16_t* k, const uint16_t* v, uint8_t* kf,
  *   s(t) = fma chain over d ascending of q[d]*k(t)[d] from 0, times scale;
  *   m = max s; e = expdet(s - m); l = 64-lane strided sums, then a
  *   butterfly; p = e * (1/l); attn_sum[t] += p in (query, head) order.
- * ws: cia_mass_workspace_bytes(S) bytes of device scratch. */
+ * ws: device scratch of ws_bytes >= cia_h2o_workspace_bytes(S, n_live)
+ * bytes (16-byte aligned); queries are processed 16 at a time through it. */
 int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uint8_t* vf,
                       const uint16_t* ks, const uint16_t* vs,
                       const int32_t* slot_pos, int n_live, uint16_t* out,
                       float* attn_sum, int S, int past, float scale, void* ws,
-                      void* stream);
+                      int64_t ws_bytes, void* stream);
+/* scratch bytes of cia_attention_h2o for S queries over up to C slots */
+int64_t cia_h2o_workspace_bytes(int S, int C);
+/* scratch bytes of cia_attention_fused's attn_sum option for S queries */
 int64_t cia_mass_workspace_bytes(int S);
 
 /* ------------------------------------------------------------------ */
@@ -257,7 +261,8 @@ typedef struct cia_layer {
   int32_t* d_slotpos;    /* device [budget], slot positions (-1: free) */
   int32_t* d_dst;        /* device [max tokens per call] */
   int n_live;
-  void* ws_mass;         /* cia_mass_workspace_bytes(max tokens per call) */
+  void* ws_mass;         /* cia_h2o_workspace_bytes(max tokens per call,
+                            budget) bytes */
 } cia_layer;
 
 /* Append S fresh tokens (k, v: device fp16 [S][8][64]) then attend q

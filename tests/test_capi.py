@@ -62,8 +62,10 @@ FAKE = 0x10000  # aligned non-null address: validation must fail before any use
     (lambda L: L.cia_attention_fused(*([None] * 7), 0, None, None, 0, 0, 0.125, None, None), 0),
     (lambda L: L.cia_kv_quant_write(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 3, None), 1),
     (lambda L: L.cia_kv_quant_write(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, None), 3),
-    (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 0, FAKE, FAKE, 1, 0, 0.125, FAKE, None), 3),
-    (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 5, FAKE, None, 1, 0, 0.125, FAKE, None), 1),
+    (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 0, FAKE, FAKE, 1, 0, 0.125, FAKE, 1 << 20, None), 3),
+    (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 5, FAKE, None, 1, 0, 0.125, FAKE, 1 << 20, None), 1),
+    (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 100, FAKE, FAKE, 1, 0, 0.125, FAKE, 64, None), 3),
+    (lambda L: L.cia_h2o_place(*([FAKE] * 9), None, 8, 2, 1, 0, None), 1),
     (lambda L: L.cia_e4m3_encode_range(0, -1, FAKE, None), 3),
     (lambda L: L.cia_e4m3_encode_range(0, 16, FAKE + 8, None), 2),
 ])

@@ -202,3 +202,45 @@ def test_h2o_decode_loop_matches_oracle(orc, cia, dev):
     assert L.n_live == C
     assert np.array_equal(L.hattn.cpu().numpy().view(np.uint32), ref.attn.view(np.uint32))
     assert np.array_equal(L.d_slotpos.cpu().numpy(), ref.slotpos)
+
+
+@pytest.mark.parametrize("n_live,S,past,seed", [(1, 1, 0, 0), (100, 1, 150, 1), (2048, 1, 5000, 2),
+                                               (300, 40, 200, 3), (4096, 17, 4000, 4)])
+def test_attention_h2o_kernel(orc, cia, dev, n_live, S, past, seed):
+    """cia_attention_h2o against the oracle on a filled slot buffer with
+    shuffled positions (some slots in the queries' future): attn_sum bit for
+    bit, outputs within 2e-3 + 1e-3|ref|; S > 16 runs several query chunks."""
+    from cuda_inf_amd import kernels as K
+    rng = np.random.default_rng(seed)
+    C = n_live + 5
+    k = torch.from_numpy(rng.standard_normal((C, 8, 64))).to(torch.float16)
+    v = torch.from_numpy(rng.standard_normal((C, 8, 64))).to(torch.float16)
+    q = torch.from_numpy(rng.standard_normal((S, 32, 64))).to(torch.float16)
+    dst = torch.arange(C, dtype=torch.int32)
+    kf = torch.zeros((C, 8, 64), dtype=torch.uint8, device=dev)
+    vf = torch.zeros_like(kf)
+    ks = torch.zeros((C, 8), dtype=torch.float16, device=dev)
+    vs = torch.zeros_like(ks)
+    K.kv_quant_write(k.to(dev), v.to(dev), kf, vf, ks, vs, dst.to(dev), C)
+    # slot positions: a permutation of past-n_live+S/2 .. so the last queries
+    # see more slots than the first
+    slot_pos = (rng.permutation(n_live) + past - n_live + S // 2).astype(np.int32)
+    slot_pos[0] = min(slot_pos[0], past)  # every query sees at least one slot
+    attn0 = np.abs(rng.standard_normal(C)).astype(np.float32)
+    rkf, rvf = kf.cpu().numpy(), vf.cpu().numpy()
+    rks, rvs = _u16(ks), _u16(vs)
+    r_attn = attn0.copy()
+    sp_full = np.concatenate([slot_pos, np.full(C - n_live, 1 << 30, np.int32)])
+    r16, r32 = orc.attention_h2o(_u16(q), rkf, rvf, rks, rvs, sp_full, n_live, r_attn, S, past)
+    d_attn = torch.from_numpy(attn0.copy()).to(dev)
+    out = torch.zeros((S, 32, 64), dtype=torch.float16, device=dev)
+    ws = torch.zeros(K.h2o_workspace_bytes(S, n_live), dtype=torch.uint8, device=dev)
+    print(f"attention_h2o n_live={n_live} S={S} past={past}", flush=True)
+    K.attention_h2o(q.to(dev), kf, vf, ks, vs, torch.from_numpy(sp_full).to(dev), n_live, out,
+                    d_attn, S, past, 0.125, ws)
+    torch.cuda.synchronize()
+    got = d_attn.cpu().numpy()
+    if not np.array_equal(got.view(np.uint32), r_attn.view(np.uint32)):
+        i = int(np.argmax(got.view(np.uint32) != r_attn.view(np.uint32)))
+        raise AssertionError(f"attn_sum differs at slot {i}: {got[i]!r} vs {r_attn[i]!r}")
+    assert_close_f16(_u16(out), r32, what="attention_h2o")
