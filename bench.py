@@ -27,6 +27,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8
 
 
 def algo_bytes(Tc: int, Tt: int) -> int:
@@ -231,14 +232,39 @@ def main():
         p1.record(stream)
         torch.cuda.synchronize()
         lms = p0.elapsed_time(p1) / reps
+        # the OCP-fp8 matrix-core variant on the same cache; its output is
+        # compared with the fp16 kernel's (the tests compare both with the
+        # fp32 restatement)
+        out8 = torch.empty_like(qp)
+        Kn.attention_fused(qp, Lp.kc8, Lp.vc8, Lp.ksc, Lp.vsc, Lp.ktail, Lp.vtail,
+                           Lp.committed, outp, None, S, 0, 0.125)
+        Kn.attention_fused_fp8(qp, Lp.kc8, Lp.vc8, Lp.ksc, Lp.vsc, Lp.ktail, Lp.vtail,
+                               Lp.committed, out8, S, 0, 0.125)
+        torch.cuda.synchronize()
+        d8 = (out8.float() - outp.float()).abs()
+        p0.record(stream)
+        for _ in range(reps):
+            Kn.attention_fused_fp8(qp, Lp.kc8, Lp.vc8, Lp.ksc, Lp.vsc, Lp.ktail, Lp.vtail,
+                                   Lp.committed, out8, S, 0, 0.125)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        f8ms = p0.elapsed_time(p1) / reps
         flops = 4.0 * D * NH * S * (S + 1) / 2
         prefill = {"tokens": S, "us": round(pms * 1e3, 1),
                    "tflops": round(flops / (pms * 1e-3) / 1e12, 2),
                    "mfma_f16_frac": round(flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                    "kernel": "attention_fused",
-                   "layer_us_with_append": round(lms * 1e3, 1)}
+                   "layer_us_with_append": round(lms * 1e3, 1),
+                   "fp8": {"kernel": "attention_fused_fp8 (v_mfma_scale_f32_16x16x128_f8f6f4)",
+                           "us": round(f8ms * 1e3, 1),
+                           "tflops": round(flops / (f8ms * 1e-3) / 1e12, 2),
+                           "mfma_fp8_frac": round(flops / (f8ms * 1e-3) / 1e12
+                                                  / MFMA_FP8_PEAK_TFLOPS, 4),
+                           "max_abs_diff_vs_fp16": round(float(d8.max()), 5),
+                           "mean_abs_diff_vs_fp16": round(float(d8.mean()), 7)}}
         log(f"prefill {S}: attention {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s; "
-            f"append + attention {lms * 1e3:.1f} us")
+            f"append + attention {lms * 1e3:.1f} us; fp8 {f8ms * 1e3:.1f} us "
+            f"({prefill['fp8']['tflops']} TFLOP/s), max |fp8 - fp16| {float(d8.max()):.4f}")
 
     cpu_layer, cpu_committed = layers[0], arr[0].committed
 

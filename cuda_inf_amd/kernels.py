@@ -80,6 +80,20 @@ def attention_fused(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out, at
          _stream())
 
 
+def attention_fused_fp8(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out, S: int,
+                        past: int, scale: float) -> None:
+    """attention_fused's causal attention on the OCP-fp8 matrix cores (Q and
+    the softmax numerators rounded to fp8; error reported, not bounded by
+    the fp16 path's tolerance)."""
+    T = past + S
+    call("cia_attention_fused_fp8", _dev(q, "q", _F16, S * NH * D),
+         _dev(kc8, "kc8", (torch.uint8,), min(T, committed) * NKV * D),
+         _dev(vc8, "vc8", (torch.uint8,), min(T, committed) * NKV * D),
+         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         committed, _dev(out, "out", _F16, S * NH * D), S, past, float(scale), _stream())
+
+
 def attn_decode_split(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int,
                       scale: float, pm, pl, po, nsplit: int = NSPLIT_DEFAULT) -> None:
     """engine.cu:396-464 with a runtime split count."""

@@ -111,6 +111,19 @@ int cia_attention_fused(const uint16_t* q, const uint8_t* kc8,
                         float* attn_sum, int S, int past, float scale,
                         void* ws, void* stream);
 
+/* The causal attention of attention_fused (engine.cu:236-308) with both
+ * products on the OCP-fp8 matrix cores (no counterpart kernel in the
+ * reference; same arguments without attn_sum/ws).  K and V are used as the
+ * cache's FP8 bytes; Q is quantised to fp8 per (query, head) with scale
+ * amax/448 and the softmax numerators per tile, so the output carries that
+ * extra rounding: its error against the fp32 reference is reported, it is
+ * not held to cia_attention_fused's tolerance. */
+int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
+                            const uint8_t* vc8, const uint16_t* ksc,
+                            const uint16_t* vsc, const uint16_t* ktail,
+                            const uint16_t* vtail, int committed, uint16_t* out,
+                            int S, int past, float scale, void* stream);
+
 /* attn_decode_split (engine.cu:396-464; launch engine.cu:848-851).
  * One query (q row 0, [32][64]) at position qpos; keys [0, qpos] are cut
  * into nsplit ranges of ceil((qpos+1)/nsplit) keys, as the reference does

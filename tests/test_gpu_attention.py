@@ -262,3 +262,44 @@ def test_decode_loop_two_layers_through_commit(orc, cia, dev):
         assert np.array_equal(_u16(L.ksc)[:c // 64], refs[l].ksc[:c // 64])
         assert np.array_equal(_u16(L.vsc)[:c // 64], refs[l].vsc[:c // 64])
         assert np.array_equal(_u16(L.ktail), refs[l].ktail)
+
+
+@pytest.mark.parametrize("S,past,outliers", [(2, 0, False), (65, 0, True), (200, 1000, True),
+                                             (17, 4079, False), (1000, 37, True), (4096, 0, True)])
+def test_prefill_fp8_error(orc, cia, dev, S, past, outliers):
+    """The OCP-fp8 matrix-core prefill on the same cache as the fp16 kernel:
+    its error against the fp32 restatement, with Q and the softmax
+    numerators rounded to fp8, is printed and bounded loosely (mean absolute
+    error below 0.01, max below 0.1); the fp16 kernel stays within
+    2e-3 + 1e-3|ref|."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    L = AttnLayer(past + S + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(past + S + 64)
+    if past:
+        q0, k0, v0 = qkv(past, seed=11, device="cpu", outliers=outliers)
+        L.forward(q0.to(dev), k0.to(dev), v0.to(dev), 0)
+        ref.append(_u16(k0), _u16(v0), 0)
+    q, k, v = qkv(S, seed=12, device="cpu", past=past, outliers=outliers)
+    qd = q.to(dev)
+    L.forward(qd, k.to(dev), v.to(dev), past)
+    ref.append(_u16(k), _u16(v), past)
+    out8 = torch.empty_like(qd)
+    print(f"prefill fp8 S={S} past={past}", flush=True)
+    K.attention_fused_fp8(qd, L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed, out8, S,
+                          past, 0.125)
+    torch.cuda.synchronize()
+    rows = None
+    if S > 1200:
+        rows = np.unique(np.concatenate([np.arange(0, 70), np.arange(S - 70, S),
+                                         np.arange(0, S, 37)])).astype(np.int32)
+    _, r32 = orc.attention_fused(_u16(q), ref, S, past, rows=rows)
+    got = out8.float().cpu().numpy()
+    if rows is not None:
+        got, r32 = got[rows], r32[rows]
+    err = np.abs(got - r32)
+    print(f"fp8 prefill S={S} past={past}: max abs err {err.max():.4g}, mean {err.mean():.4g}, "
+          f"max rel {(err / (np.abs(r32) + 1e-3)).max():.3g}")
+    assert np.isfinite(got).all()
+    assert err.mean() < 0.01 and err.max() < 0.1
