@@ -180,3 +180,11 @@ def attention_h2o(q, kf, vf, ks, vs, slot_pos, n_live: int, out, attn_sum, S: in
          _dev(out, "out", _F16, S * NH * D), _dev(attn_sum, "attn_sum", (torch.float32,), n_live),
          S, past, float(scale), _dev(ws, "ws", (torch.uint8,), h2o_workspace_bytes(S, n_live)),
          ws.numel(), _stream())
+
+
+# ------------------------------------------------------------ QK producers
+def qk_norm_rope(q, k, qw, kw, pos, S: int, eps: float = 1e-5, theta: float = 5.0e6) -> None:
+    """engine.cu:799-801 (rmsnorm_head on q and k, then rope) in place, one launch."""
+    call("cia_qk_norm_rope", _dev(q, "q", _F16, S * NH * D), _dev(k, "k", _F16, S * NKV * D),
+         _dev(qw, "qw", _F16, D), _dev(kw, "kw", _F16, D), _dev(pos, "pos", (torch.int32,), S),
+         S, float(eps), float(theta), _stream())

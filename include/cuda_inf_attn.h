@@ -214,6 +214,22 @@ int64_t cia_h2o_workspace_bytes(int S, int C);
 int64_t cia_mass_workspace_bytes(int S);
 
 /* ------------------------------------------------------------------ */
+/* QK producers                                                       */
+/* ------------------------------------------------------------------ */
+
+/* rmsnorm_head on q, rmsnorm_head on k, then rope (engine.cu:148-182;
+ * launches engine.cu:799-801) as one launch, in place on q [S][32][64] and
+ * k [S][8][64].  qw, kw: fp16 [64] norm weights; pos: device int32 [S].
+ * Fixed-order arithmetic (bit-identical to the CPU restatement): the sum of
+ * squares in the reference's tree order, inv = 1/sqrtf(ss/64 + eps),
+ * y = fp16((x*inv)*w); RoPE angles pos * theta^(-2d/64) (the exponent table
+ * in double, rounded to fp32) with a deterministic sin/cos in place of
+ * sinf/cosf; fp16 results after each stage as in the reference. */
+int cia_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* qw,
+                     const uint16_t* kw, const int32_t* pos, int S, float eps,
+                     float theta, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* host-side policy (plain C++, no device access)                     */
 /* ------------------------------------------------------------------ */
 

@@ -59,6 +59,9 @@ def _declare(L):
         "orc_e4m3_encode_array": (None, [_P, _P, _I64]),
         "orc_e4m3_encode_range_u32": (None, [ctypes.c_uint32, _I64, _P]),
         "orc_exp_det_array": (None, [_P, _P, _I64]),
+        "orc_sincos_det_array": (None, [_P, _P, _P, _I64]),
+        "orc_rope_invf": (None, [_F, _P]),
+        "orc_qk_norm_rope": (None, [_P, _P, _P, _P, _P, _I, _F, _F]),
         "orc_kv_write_tail": (None, [_P, _P, _P, _P, _I, _I]),
         "orc_kv_commit_group": (None, [_P, _P, _P, _P, _P, _P, _I, _I]),
         "orc_kv_append": (_I, [_P] * 8 + [_P, _I, _I]),
@@ -123,6 +126,32 @@ def exp_det(x: np.ndarray) -> np.ndarray:
 
 def quant_scale(amax: float) -> float:
     return lib().orc_quant_scale(amax)
+
+
+def sincos_det(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    s = np.empty(x.shape, np.float32)
+    c = np.empty(x.shape, np.float32)
+    lib().orc_sincos_det_array(_p(x), _p(s), _p(c), x.size)
+    return s, c
+
+
+def rope_invf(theta: float = 5.0e6) -> np.ndarray:
+    out = np.empty(32, np.float32)
+    lib().orc_rope_invf(theta, _p(out))
+    return out
+
+
+def qk_norm_rope(q, k, qw, kw, pos, eps: float = 1e-5, theta: float = 5.0e6):
+    """engine.cu:799-801 (RMSNorm of q and k, then RoPE) with the
+    deterministic sin/cos; returns new fp16 bit arrays."""
+    q = np.array(_u16(q), dtype=np.uint16, copy=True, order="C")
+    k = np.array(_u16(k), dtype=np.uint16, copy=True, order="C")
+    qw = np.ascontiguousarray(_u16(qw), dtype=np.uint16)
+    kw = np.ascontiguousarray(_u16(kw), dtype=np.uint16)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().orc_qk_norm_rope(_p(q), _p(k), _p(qw), _p(kw), _p(pos), int(pos.size), eps, theta)
+    return q, k
 
 
 # ---------------------------------------------------------------- cache

@@ -40,6 +40,15 @@
  *                         constructions that force known masses.
  *   h2o_pick_slots        hand-checked cases: lowest-slot tie break, the
  *                         window rule pos <= posj - W, the fallback scan.
+ *   sincos_det            error against float64 sin/cos (<= 2e-7 up to
+ *                         2.6e5), exact values at 0, odd/even symmetry bit
+ *                         for bit, sin^2 + cos^2 = 1.
+ *   rope_invf             float32 rounding of float64 theta^(-2i/64).
+ *   qk_norm_rope          an independent numpy float32 restatement of the
+ *                         norm (tree-ordered sum of squares) and rotation;
+ *                         unit-RMS rows, pair norms kept, position 0 is the
+ *                         identity; within one fp16 step of the torch
+ *                         producers (fp32 torch cos/sin).
  *
  * Deterministic attention mass (used where the reference accumulates
  * attn_sum with atomicAdd, engine.cu:291-307, 371-383).  The reference's sum
@@ -206,6 +215,71 @@ ORC_HOT float orc_exp_det(float x) {
   p = fmaf(p, r, 1.0f);
   int k = (int)kf;
   return p * u2f((uint32_t)(k + 127) << 23);
+}
+
+static inline float h2f_(uint16_t h) { return orc_f16_to_f32(h); }
+
+/* ------------------------------------------------------------------ */
+/* deterministic sin / cos and the QK producers                       */
+/* ------------------------------------------------------------------ */
+void orc_sincos_det(float x, float* s, float* c) {
+  const float kf = rintf(x * 0x1.45f306p-1f);    /* x * 2/pi */
+  float r = fmaf(-kf, 0x1.921fb6p+0f, x);         /* pi/2 in three parts */
+  r = fmaf(-kf, -0x1.777a5cp-25f, r);
+  r = fmaf(-kf, -0x1.ee59dap-50f, r);
+  const float r2 = r * r;
+  float ps = fmaf(r2, 0x1.71de3ap-19f, -0x1.a01a02p-13f); /* 1/9!, -1/7! */
+  ps = fmaf(r2, ps, 0x1.111112p-7f);                      /* 1/5! */
+  ps = fmaf(r2, ps, -0x1.555556p-3f);                     /* -1/3! */
+  const float sr = fmaf(r * r2, ps, r);
+  float pc = fmaf(r2, 0x1.a01a02p-16f, -0x1.6c16c2p-10f); /* 1/8!, -1/6! */
+  pc = fmaf(r2, pc, 0x1.555556p-5f);                      /* 1/4! */
+  pc = fmaf(r2, pc, -0x1p-1f);                            /* -1/2 */
+  const float cr = fmaf(r2, pc, 1.0f);
+  switch (((int)kf) & 3) {
+    case 0: *s = sr; *c = cr; break;
+    case 1: *s = cr; *c = -sr; break;
+    case 2: *s = -sr; *c = -cr; break;
+    default: *s = -cr; *c = sr; break;
+  }
+}
+
+void orc_rope_invf(float theta, float* invf32) {
+  for (int i = 0; i < D / 2; i++) invf32[i] = (float)pow((double)theta, -(2.0 * i) / D);
+}
+
+/* one head row in place: RMSNorm (tree order of engine.cu:153-154) then RoPE */
+static void qk_row(uint16_t* row, const uint16_t* w, int32_t pos, float eps, const float* invf) {
+  float v[D], y[D];
+  for (int d = 0; d < D; d++) {
+    const float x = h2f_(row[d]);
+    v[d] = x * x;
+  }
+  for (int st = D / 2; st > 0; st >>= 1)
+    for (int d = 0; d < st; d++) v[d] = v[d] + v[d + st];
+  const float inv = 1.0f / sqrtf(v[0] / (float)D + eps);
+  for (int d = 0; d < D; d++) y[d] = h2f_(orc_f32_to_f16((h2f_(row[d]) * inv) * h2f_(w[d])));
+  for (int d = 0; d < D / 2; d++) {
+    float sn, cs;
+    orc_sincos_det((float)pos * invf[d], &sn, &cs);
+    const float x0 = y[d], x1 = y[d + D / 2];
+    row[d] = orc_f32_to_f16(x0 * cs - x1 * sn);
+    row[d + D / 2] = orc_f32_to_f16(x1 * cs + x0 * sn);
+  }
+}
+
+void orc_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* qw, const uint16_t* kw,
+                      const int32_t* pos, int S, float eps, float theta) {
+  float invf[D / 2];
+  orc_rope_invf(theta, invf);
+  for (int i = 0; i < S; i++) {
+    for (int h = 0; h < NH; h++) qk_row(q + ((size_t)i * NH + h) * D, qw, pos[i], eps, invf);
+    for (int h = 0; h < NKV; h++) qk_row(k + ((size_t)i * NKV + h) * D, kw, pos[i], eps, invf);
+  }
+}
+
+void orc_sincos_det_array(const float* x, float* s, float* c, int64_t n) {
+  for (int64_t i = 0; i < n; i++) orc_sincos_det(x[i], &s[i], &c[i]);
 }
 
 void orc_f32_to_f16_array(const float* x, uint16_t* out, int64_t n) {

@@ -56,11 +56,31 @@ float orc_quant_scale(float amax);
  * the H2O attention-mass definition uses it on both CPU and GPU. */
 float orc_exp_det(float x);
 
+/* deterministic sin and cos of an fp32 angle (|x| < 2^20): k = rint(x*2/pi),
+ * three-part Cody-Waite reduction with fma, Taylor polynomials (degree 9 /
+ * 8, Horner with fma), quadrant by k & 3.  Used by the deterministic RoPE
+ * on both CPU and GPU in place of engine.cu:167-168's sinf/cosf. */
+void orc_sincos_det(float x, float* s, float* c);
+/* RoPE inverse frequencies theta^(-2i/64), i = 0..31, computed in double
+ * and rounded to fp32 (engine.cu:166's powf as a table). */
+void orc_rope_invf(float theta, float* invf32);
+/* Per-head RMSNorm then rotate-half RoPE, in place on q [S][NH][D] and
+ * k [S][NKV][D] (engine.cu:148-158 twice, then 161-182, called at
+ * 799-801): ss = the reference's tree sum of x^2 (pairs d, d+s for
+ * s = 32..1), inv = 1/sqrtf(ss/64 + eps), y = fp16((x*inv)*w); then for
+ * d < 32, ang = pos*invf[d], (sn, cs) = sincos_det(ang),
+ * y0' = fp16(y0*cs - y1*sn), y1' = fp16(y1*cs + y0*sn), each product and
+ * difference rounded separately.  qw, kw: fp16 [64] norm weights. */
+void orc_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* qw,
+                      const uint16_t* kw, const int32_t* pos, int S, float eps,
+                      float theta);
+
 /* bulk helpers (for exhaustive tests through ctypes) */
 void orc_f32_to_f16_array(const float* x, uint16_t* out, int64_t n);
 void orc_e4m3_encode_array(const float* x, uint8_t* out, int64_t n);
 void orc_e4m3_encode_range_u32(uint32_t first_bits, int64_t n, uint8_t* out);
 void orc_exp_det_array(const float* x, float* out, int64_t n);
+void orc_sincos_det_array(const float* x, float* s, float* c, int64_t n);
 
 /* ---- group-64 KV cache ---------------------------------------------- */
 /* engine.cu:190-198 */
