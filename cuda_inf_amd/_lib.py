@@ -116,4 +116,5 @@ class cia_layer(ctypes.Structure):
         ("budget", _I), ("window", _I),
         ("kf", _P), ("vf", _P), ("ks", _P), ("vs", _P), ("hattn", _P), ("d_slotpos", _P),
         ("d_dst", _P), ("n_live", _I), ("ws_mass", _P),
+        ("qw", _P), ("kw", _P), ("eps", _F), ("theta", _F), ("prep_ws", _P), ("prep_cap", _I),
     ]

@@ -109,7 +109,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
-    int64_t ws_bytes, void* stream, void* mid_event);
+    int64_t ws_bytes, void* stream, void* mid_event, const void* prep);
 
 extern "C" int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                                const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
@@ -122,7 +122,8 @@ extern "C" int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint
   CIA_REQUIRE(qpos >= 0 && ws_bytes >= 0, CIA_ERR_ARG);
   CIA_REQUIRE(committed <= qpos + 1 && qpos - committed < G, CIA_ERR_STATE);
   return cia_decode_mfma(q, kc8, vc8, ksc, vsc, (uint16_t*)ktail, (uint16_t*)vtail, nullptr,
-                         nullptr, committed, qpos, scale, out, ws, ws_bytes, stream, nullptr);
+                         nullptr, committed, qpos, scale, out, ws, ws_bytes, stream, nullptr,
+                         nullptr);
 }
 
 // attn_sum support lives in mass.hip

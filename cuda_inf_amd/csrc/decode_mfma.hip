@@ -33,6 +33,7 @@
 //   (Workgroup-to-workgroup synchronisation inside one launch costs more on
 //   this part than a kernel boundary, hence the second launch.)
 #include "attn_range.h"
+#include "qk_prep.h"
 
 namespace cia {
 
@@ -76,6 +77,8 @@ struct DecodeArgs {
   int npairs;     // committed / 32
   int nwg;        // workgroups per half
   uint16_t* out;  // [32][64]
+  QkPrep prep;    // prep.qw != null: q and the fresh k arrive raw and are
+                  // normalised and rotated here (engine.cu:799-801)
 };
 
 // ---------------------------------------------------------------- attend
@@ -84,9 +87,24 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   __shared__ __attribute__((aligned(16))) uint8_t klds[kDecWaves][32 * 256];
   __shared__ __attribute__((aligned(16))) uint8_t vlds[kDecWaves][32 * 256];
   __shared__ float sm[kDecWaves][16], sl[kDecWaves][16];
+  __shared__ __attribute__((aligned(16))) uint16_t qprep[16 * D];
   const int half = blockIdx.y;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int n = l & 15, b = l >> 4;  // MFMA column / k-group of this lane
+  if (a.prep.qw) {
+    // the QK producers on the half's 16 query heads: two per wave, one dim
+    // per lane, into LDS
+    float sn, cs;
+    rope_sincos(l, a.qpos, a.prep.rt, sn, cs);
+    const float wq = h2f(a.prep.qw[l]);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int hh = 2 * w + r;
+      qprep[hh * D + l] =
+          qk_norm_rope_sc(h2f(a.q[(size_t)(half * 16 + hh) * D + l]), wq, l, sn, cs, a.prep.eps);
+    }
+    __syncthreads();
+  }
   uint8_t* kw = klds[w];
   uint8_t* vw = vlds[w];
   // this wave's pairs: an even share of the half's pairs
@@ -96,7 +114,10 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   const int p1 = (int)(((long long)(wid + 1) * a.npairs) / nwaves);
   // Q^T as the block-diagonal B operand, fp16
   f16x8 qop[8];
-  if ((n >> 2) == b) {
+  if ((n >> 2) == b && a.prep.qw) {
+#pragma unroll
+    for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qprep + n * D + 8 * mu);
+  } else if ((n >> 2) == b) {
     const uint16_t* qp = a.q + (size_t)(half * 16 + n) * D;
 #pragma unroll
     for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qp + 8 * mu);
@@ -249,6 +270,22 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   const int h = (blockIdx.x & 7) * 4 + (j >> 3), c = j & 7, kvh = h / GQA;
   const int l = threadIdx.x;
   const int ntail = a.qpos + 1 - a.committed;  // 0..64
+  // the QK producers on this head's q row and the fresh k row (one dim per
+  // lane) when they arrive raw
+  __shared__ __attribute__((aligned(16))) uint16_t prep[2 * D];
+  const bool raw = a.prep.qw != nullptr;
+  if (raw) {
+    float sn, cs;
+    rope_sincos(l, a.qpos, a.prep.rt, sn, cs);
+    prep[l] = qk_norm_rope_sc(h2f(a.q[(size_t)h * D + l]), h2f(a.prep.qw[l]), l, sn, cs,
+                              a.prep.eps);
+    if (a.knew)
+      prep[D + l] = qk_norm_rope_sc(h2f(a.knew[(size_t)kvh * D + l]), h2f(a.prep.kw[l]), l, sn,
+                                    cs, a.prep.eps);
+    __syncthreads();
+  }
+  const uint16_t* qrow = raw ? prep : a.q + (size_t)h * D;
+  const uint16_t* knew = raw ? prep + D : (a.knew ? a.knew + (size_t)kvh * D : nullptr);
   // ---- every load first: partials, then the tail row of this lane
   const float* ph = a.part + (size_t)h * a.nwg * kPart;
   float pm[2], pl[2];
@@ -274,9 +311,9 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   const bool commit = a.knew && ntail == G;
   if (live) {
     const bool fresh = a.knew && l == ntail - 1;
-    const uint16_t* kp = fresh ? a.knew + kvh * D : a.ktail + ((size_t)l * NKV + kvh) * D;
+    const uint16_t* kp = fresh ? knew : a.ktail + ((size_t)l * NKV + kvh) * D;
     const uint16_t* vp = fresh ? a.vnew + kvh * D : a.vtail + ((size_t)l * NKV + kvh) * D;
-    const uint16_t* qp = a.q + (size_t)h * D;
+    const uint16_t* qp = qrow;
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) {
       kq[cc] = *(const u32x4*)(kp + 8 * cc);
@@ -293,7 +330,7 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   if (a.knew && c == 0 && h % GQA == 0 && l < 16) {
     const int row = ntail - 1, cc = l & 7;
     uint16_t* dst = (l < 8 ? a.ktail : a.vtail) + ((size_t)row * NKV + kvh) * D + cc * 8;
-    const uint16_t* src = (l < 8 ? a.knew : a.vnew) + kvh * D + cc * 8;
+    const uint16_t* src = (l < 8 ? knew : a.vnew + kvh * D) + cc * 8;
     *(u32x4*)dst = *(const u32x4*)src;
   }
   // ---- tail scores (log2 units) and this lane's V values (dims 8c..8c+7)
@@ -437,16 +474,18 @@ extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
 // tail write of the fresh token fused in.  Internal entry shared by
 // cia_attn_decode and the layer driver; mid_event (may be NULL) is recorded
 // between the two launches, for per-kernel timing.
+// prep (may be NULL): a QkPrep when q and knew arrive raw.
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
-    int64_t ws_bytes, void* stream, void* mid_event) {
+    int64_t ws_bytes, void* stream, void* mid_event, const void* prep) {
   const int npairs = committed / 32;
   const int nwg = dec_nwg(npairs);
   if ((int64_t)NH * nwg * kPart * (int64_t)sizeof(float) > ws_bytes) return CIA_ERR_ARG;
   DecodeArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail, knew, vnew, committed, qpos, scale,
-                (float*)ws, npairs, nwg, out};
+                (float*)ws, npairs, nwg, out, QkPrep{}};
+  if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_decode_attend, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
   int st = launch_status();

@@ -19,7 +19,14 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
-    int64_t ws_bytes, void* stream, void* mid_event);
+    int64_t ws_bytes, void* stream, void* mid_event, const void* prep);
+
+extern "C" __attribute__((visibility("hidden"))) int cia_qk_prep_into(
+    const uint16_t* q, const uint16_t* k, const uint16_t* qw, const uint16_t* kw, uint16_t* oq,
+    uint16_t* ok, int pos0, int S, float eps, float theta, void* stream);
+
+extern "C" __attribute__((visibility("hidden"))) const void* cia_qk_prep_desc(
+    const uint16_t* qw, const uint16_t* kw, float eps, float theta);
 
 namespace cia {
 
@@ -139,6 +146,35 @@ extern "C" int cia_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos, f
 // ---------------------------------------------------------------- layer driver
 namespace {
 
+// A layer with QK producers (qw set) must have them complete
+int prep_check(const cia_layer* L) {
+  if (!L->qw) return CIA_OK;
+  if (!L->kw) return CIA_ERR_NULL;
+  if (!(L->eps >= 0.0f) || !(L->theta > 0.0f) || L->theta == __builtin_inff()) return CIA_ERR_ARG;
+  return CIA_OK;
+}
+
+// engine.cu:799-801 for the unfused paths: the producers run into the
+// layer's prep_ws and q / k then point at the prepared rows
+int prep_qk(cia_layer* L, const uint16_t*& q, const uint16_t*& k, int S, int past,
+            void* stream) {
+  if (!L->qw) return CIA_OK;
+  if (!L->prep_ws) return CIA_ERR_NULL;
+  if (S > L->prep_cap) return CIA_ERR_ARG;
+  uint16_t* oq = L->prep_ws;
+  uint16_t* ok = L->prep_ws + (size_t)L->prep_cap * CIA_NH * CIA_HEAD_DIM;
+  const int st = cia_qk_prep_into(q, k, L->qw, L->kw, oq, ok, past, S, L->eps, L->theta, stream);
+  if (st) return st;
+  q = oq;
+  k = ok;
+  return CIA_OK;
+}
+
+// the decode kernels' descriptor when they run the producers themselves
+const void* layer_prep(const cia_layer* L) {
+  return L->qw ? cia_qk_prep_desc(L->qw, L->kw, L->eps, L->theta) : nullptr;
+}
+
 // engine.cu:803-828 with the slot choice on the device: place + quantise,
 // then attention with the mass update; no host round trip
 int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -149,7 +185,9 @@ int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16
       !L->ws_mass)
     return CIA_ERR_NULL;
   const int n0 = L->n_live;
-  int st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
+  int st = prep_qk(L, q, k, S, past, stream);
+  if (st) return st;
+  st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
                          &L->n_live, C, L->window, S, past, stream);
   if (st) return st;
   if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
@@ -198,7 +236,7 @@ int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int pa
     if (L->committed > past + 1 || past - L->committed >= CIA_KVGROUP) return CIA_ERR_STATE;
     return cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, nullptr,
                            nullptr, L->committed, past, scale, out, L->ws_decode,
-                           cia_decode_workspace_bytes(L->maxT), stream, mid_event);
+                           cia_decode_workspace_bytes(L->maxT), stream, mid_event, nullptr);
   }
   int st = cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail,
                                L->committed, out, nullptr, S, past, scale, nullptr, stream);
@@ -220,9 +258,11 @@ bool fused_append_ok(const cia_layer* L, int past) {
 int decode_fused_append(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         uint16_t* out, int past, float scale, void* stream,
                         void* mid_event = nullptr) {
+  // q and k arrive raw on a layer with producers: the decode kernels run them
   const int st = cia_decode_mfma(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail, k, v,
                                  L->committed, past, scale, out, L->ws_decode,
-                                 cia_decode_workspace_bytes(L->maxT), stream, mid_event);
+                                 cia_decode_workspace_bytes(L->maxT), stream, mid_event,
+                                 layer_prep(L));
   if (st == CIA_OK && past - L->committed == CIA_KVGROUP - 1) L->committed += CIA_KVGROUP;
   return st;
 }
@@ -235,10 +275,13 @@ extern "C" int cia_layer_forward(cia_layer* L, const uint16_t* q, const uint16_t
   if (!L || !q || !k || !v || !out) return CIA_ERR_NULL;
   if (S < 1 || past < 0) return CIA_ERR_ARG;
   if (evicted) *evicted = -1;
+  int st = prep_check(L);
+  if (st) return st;
   if (L->budget > 0) return h2o_forward(L, q, k, v, out, S, past, scale, evicted, stream);
   if (S == 1 && fused_append_ok(L, past))
     return decode_fused_append(L, q, k, v, out, past, scale, stream);
-  int st = group64_append(L, k, v, S, past, stream);
+  if ((st = prep_qk(L, q, k, S, past, stream))) return st;
+  st = group64_append(L, k, v, S, past, stream);
   if (st) return st;
   return group64_attend(L, q, out, S, past, scale, stream);
 }
@@ -248,6 +291,7 @@ extern "C" int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t*
   if (!L || !k || !v) return CIA_ERR_NULL;
   if (S < 0 || past < 0) return CIA_ERR_ARG;
   if (L->budget > 0) return CIA_ERR_STATE;  // H2O layers place tokens by policy
+  if (L->qw) return CIA_ERR_STATE;  // raw k needs its q: use cia_layer_forward
   return S ? group64_append(L, k, v, S, past, stream) : CIA_OK;
 }
 
@@ -256,6 +300,10 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
                                int steps, float scale, void** events, void* stream) {
   if (!layers || !q || !k || !v || !out) return CIA_ERR_NULL;
   if (n_layers < 1 || steps < 0 || past < 0) return CIA_ERR_ARG;
+  for (int l = 0; l < n_layers; l++) {
+    const int st = prep_check(&layers[l]);
+    if (st) return st;
+  }
   const size_t qrow = (size_t)CIA_NH * CIA_HEAD_DIM, krow = (size_t)CIA_NKV * CIA_HEAD_DIM;
   hipStream_t s = (hipStream_t)stream;
   for (int i = 0; i < steps; i++) {
@@ -273,15 +321,18 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
         continue;
       }
       const bool fused = fused_append_ok(L, pos);
+      const uint16_t* qi = q + r * qrow;
+      const uint16_t* ki = k + r * krow;
       if (!fused) {
-        st = group64_append(L, k + r * krow, v + r * krow, 1, pos, stream);
+        if ((st = prep_qk(L, qi, ki, 1, pos, stream))) return st;
+        st = group64_append(L, ki, v + r * krow, 1, pos, stream);
         if (st) return st;
       }
       void* mid = events ? events[3 * r + 1] : nullptr;
       if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r], s)))) return st;
-      st = fused ? decode_fused_append(L, q + r * qrow, k + r * krow, v + r * krow,
-                                       out + r * qrow, pos, scale, stream, mid)
-                 : group64_attend(L, q + r * qrow, out + r * qrow, 1, pos, scale, stream, mid);
+      st = fused ? decode_fused_append(L, qi, ki, v + r * krow, out + r * qrow, pos, scale,
+                                       stream, mid)
+                 : group64_attend(L, qi, out + r * qrow, 1, pos, scale, stream, mid);
       if (st) return st;
       if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
     }

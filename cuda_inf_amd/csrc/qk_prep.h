@@ -54,20 +54,41 @@ __device__ __forceinline__ float fp32_round(float v) {
   return v;
 }
 
-// One head row, lane d holding x = row[d] and w = weight[d]: returns the
-// fp16 bits of the normalised, rotated value of dim d.  Called by all 64
-// lanes of a wave together.
-__device__ __forceinline__ uint16_t qk_norm_rope_lane(float x, float w, int d, int pos,
-                                                      float eps, const RopeTable& rt) {
+// The rotation of lane d's frequency (d mod 32) at position pos
+__device__ __forceinline__ void rope_sincos(int d, int pos, const RopeTable& rt, float& sn,
+                                            float& cs) {
+#pragma clang fp contract(off)
+  sincos_det((float)pos * rt.invf[d & 31], sn, cs);
+}
+
+// One head row, lane d holding x = row[d] and w = weight[d], (sn, cs) the
+// rotation of lane d's frequency: returns the fp16 bits of the normalised,
+// rotated value of dim d.  Called by all 64 lanes of a wave together.
+__device__ __forceinline__ uint16_t qk_norm_rope_sc(float x, float w, int d, float sn, float cs,
+                                                    float eps) {
 #pragma clang fp contract(off)
   const float ss = wave_sum(x * x);
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
   const float y = h2f(f2h(fp32_round((x * inv) * w)));
   const float other = __shfl_xor(y, 32);
-  float sn, cs;
-  sincos_det((float)pos * rt.invf[d & 31], sn, cs);
   const float r = d < 32 ? y * cs - other * sn : y * cs + other * sn;
   return f2h(fp32_round(r));
 }
+
+__device__ __forceinline__ uint16_t qk_norm_rope_lane(float x, float w, int d, int pos,
+                                                      float eps, const RopeTable& rt) {
+  float sn, cs;
+  rope_sincos(d, pos, rt, sn, cs);
+  return qk_norm_rope_sc(x, w, d, sn, cs, eps);
+}
+
+// What the decode kernels need to run the QK producers on the raw q / fresh
+// k themselves; qw == nullptr: q and k arrive prepared.
+struct QkPrep {
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
+  RopeTable rt;
+};
 
 }  // namespace cia

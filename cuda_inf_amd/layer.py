@@ -63,11 +63,16 @@ class AttnLayer:
     library's own split (and the tail write fused into it).  ``budget`` > 0
     enables H2O eviction with a ``budget``-slot buffer and local ``window``
     (0 -> budget/2, clamped as the reference does against ``prompt_len``).
+    ``qk_norm`` = (q weight, k weight), fp16 [64] each: q and k passed to
+    ``forward`` are raw and the layer runs the QK producers (per-head
+    RMSNorm with ``eps``, RoPE at ``theta``; engine.cu:799-801) itself --
+    inside the decode kernels for single-token steps, else one launch into a
+    ``max_batch``-token scratch.
     """
 
     def __init__(self, max_tokens: int, *, nsplit: int = NSPLIT_DEFAULT, budget: int = 0,
                  window: int = 0, prompt_len: int = 0, max_batch: int = 4096,
-                 device="cuda"):
+                 qk_norm=None, eps: float = 1e-5, theta: float = 5.0e6, device="cuda"):
         dev = torch.device(device)
         self.device = dev
         self.maxT = max_tokens
@@ -106,6 +111,15 @@ class AttnLayer:
             for name in ("kf", "vf", "ks", "vs", "hattn", "d_slotpos", "d_dst", "ws_mass"):
                 setattr(s, name, getattr(self, name).data_ptr())
             s.n_live = 0
+        if qk_norm is not None:
+            qw, kw = qk_norm
+            self.qw = torch.as_tensor(qw).to(device=dev, dtype=f16).contiguous()
+            self.kw = torch.as_tensor(kw).to(device=dev, dtype=f16).contiguous()
+            assert self.qw.numel() == D and self.kw.numel() == D
+            self.prep_ws = torch.zeros(max_batch * (NH + NKV) * D, dtype=f16, device=dev)
+            s.qw, s.kw = self.qw.data_ptr(), self.kw.data_ptr()
+            s.eps, s.theta = float(eps), float(theta)
+            s.prep_ws, s.prep_cap = self.prep_ws.data_ptr(), max_batch
         self.max_batch = max_batch
         self._s = s
 
@@ -124,7 +138,7 @@ class AttnLayer:
         On an H2O layer the evicted slot is read back from the device, which
         waits for the stream; ``evicted=False`` skips that (returns None)."""
         S = k.shape[0]
-        if self.budget and S > self.max_batch:
+        if (self.budget or self._s.qw) and S > self.max_batch:
             raise ValueError(f"S={S} exceeds max_batch={self.max_batch}")
         for t, name, n in ((q, "q", S * NH * D), (k, "k", S * NKV * D), (v, "v", S * NKV * D)):
             if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous() or t.numel() != n:

@@ -292,10 +292,21 @@ typedef struct cia_layer {
   int n_live;
   void* ws_mass;         /* cia_h2o_workspace_bytes(max tokens per call,
                             budget) bytes */
+  /* QK producers (engine.cu:799-801); qw == NULL: q and k arrive prepared.
+   * Otherwise q and k are raw and the layer runs per-head RMSNorm (weights
+   * qw, kw: fp16 [64], eps) and RoPE (theta) at positions past..past+S-1
+   * itself: inside the decode kernels for a single-token step on the
+   * group-64 cache, else with one cia_qk_norm_rope launch into prep_ws
+   * (device fp16 [prep_cap][40][64], q rows then k rows per token). */
+  const uint16_t* qw; const uint16_t* kw;
+  float eps, theta;
+  uint16_t* prep_ws;
+  int prep_cap;
 } cia_layer;
 
 /* Append S fresh tokens (k, v: device fp16 [S][8][64]) then attend q
- * (device fp16 [S][32][64]) into out, exactly as engine.cu:802-857:
+ * (device fp16 [S][32][64]) into out, exactly as engine.cu:799-857 (with
+ * the QK producers when L->qw is set; q and k are then only read):
  * H2O when budget > 0, else append + (S == 1 ? flash-decoding : fused).
  * H2O mode chooses slots on the device (cia_h2o_place) where the reference
  * blocks on copies (engine.cu:814, 824-825).  evicted (may be NULL): on
