@@ -64,6 +64,9 @@ def main():
     ap.add_argument("--long-ctx", type=int, default=131072,
                     help="long-context decode leg: context tokens (0 = skip)")
     ap.add_argument("--long-steps", type=int, default=8)
+    ap.add_argument("--prep-steps", type=int, default=64,
+                    help="decode tokens with the QK producers run inside the decode kernels "
+                         "(raw q/k in; 0 = skip)")
     ap.add_argument("--h2o-steps", type=int, default=4000,
                     help="H2O decode steps after a 1024-token prompt (0 = skip)")
     ap.add_argument("--calib-copy", type=int, default=0,
@@ -83,7 +86,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
-    total_steps = W + 2 * K + a.cold_steps
+    total_steps = W + 2 * K + a.cold_steps + a.prep_steps
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
@@ -204,6 +207,36 @@ def main():
         log(f"cold: median {cold_us:.2f} us/token")
     mean_tok_bytes = timed_bytes / K
 
+    # ---- QK producers fused: the same layers take raw q / k, and the decode
+    # kernels run per-head RMSNorm + RoPE (engine.cu:799-801) themselves
+    prep = None
+    if a.prep_steps > 0:
+        g8 = workload.generator(17, dev)
+        qw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        kw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        prep_ws = [torch.zeros((NH + NKV) * D, dtype=torch.float16, device=dev) for _ in range(nL)]
+        for l in range(nL):
+            arr[l].qw, arr[l].kw = qw.data_ptr(), kw.data_ptr()
+            arr[l].eps, arr[l].theta = workload.EPS, workload.ROPE_THETA
+            arr[l].prep_ws, arr[l].prep_cap = prep_ws[l].data_ptr(), 1
+        run(2)
+        torch.cuda.synchronize()
+        n = a.prep_steps - 2
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        run(n)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        prep_us = c0.elapsed_time(c1) * 1e3 / n
+        for l in range(nL):
+            arr[l].qw = arr[l].kw = arr[l].prep_ws = None
+            arr[l].prep_cap = 0
+        prep = {"us_per_token": round(prep_us, 2), "tokens": n,
+                "over_prepared_inputs_us": round(prep_us - us_tok, 2),
+                "kernels": "producers inside k_decode_attend / k_decode_finish"}
+        log(f"decode with fused QK producers: {prep_us:.2f} us/token "
+            f"({prep_us - us_tok:+.2f} against prepared inputs)")
+
     # ---- prefill leg: causal attention_fused over a fresh cache
     prefill = None
     if a.prefill > 0:
@@ -315,6 +348,7 @@ def main():
                      "event_bracketed_us": {"k_decode_attend": round(att_us, 3),
                                             "k_decode_finish": round(fin_us, 3)}},
         "prefill": prefill,
+        "qk_producers_fused": prep,
         "long_context": long_ctx,
         "h2o": h2o,
         "cpu_baseline": cpu,

@@ -120,8 +120,11 @@ __device__ __forceinline__ float fast_exp(float x) {
 
 // ---------------------------------------------------------------- waves
 // Cross-lane steps without the LDS unit: DPP row rotations within each
-// 16-lane row, then v_permlane16_swap / v_permlane32_swap across rows (each
-// returns, per lane, its own value and that of lane l ^ 16 / l ^ 32).
+// 16-lane row, then v_permlane16_swap / v_permlane32_swap across rows.  Each
+// swap returns a pair holding, per lane, its own value and that of lane
+// l ^ 16 / l ^ 32: the partner is the second element in the lower row of
+// each swapped pair of rows (lanes 0-15, 32-47 / lanes 0-31) and the first
+// element in the upper one.
 template <int kN>
 __device__ __forceinline__ float row_ror(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
@@ -166,6 +169,22 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
   v += row_ror<2>(v);
   v += row_ror<1>(v);
   return col4_sum(v);
+}
+
+// Sum over the wave in the tree order red[d] += red[d + s], s = 32, 16, ..,
+// 1 (the shared-memory reduction of engine.cu:153-154), every add "lower
+// lane + upper lane"; lanes d < s hold the tree's values at each level and
+// lane 0's total is broadcast.  No LDS traffic.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+  // (a row rotation by 16 - k hands lane i the value of lane i + k of its
+  // 16-lane row for i < 16 - k)
+  v = v + swap32(v)[1];    // lane d < 32: v[d] + v[d + 32]
+  v = v + swap16(v)[1];    // lane d < 16: + (v[d + 16] + v[d + 48])
+  v = v + row_ror<8>(v);   // lane d < 8: + lane d + 8
+  v = v + row_ror<12>(v);  // lane d < 4: + lane d + 4
+  v = v + row_ror<14>(v);  // lane d < 2: + lane d + 2
+  v = v + row_ror<15>(v);  // lane 0: + lane 1
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
 // butterfly max / sum (xor 32, 16, ..., 1): the fixed order of the

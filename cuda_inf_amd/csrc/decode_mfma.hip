@@ -83,6 +83,8 @@ struct DecodeArgs {
 
 // ---------------------------------------------------------------- attend
 // grid = (nwg, 2 halves), block = 64 * kDecWaves
+// kPrep: q arrives raw and the QK producers run here (a.prep)
+template <bool kPrep>
 __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t klds[kDecWaves][32 * 256];
   __shared__ __attribute__((aligned(16))) uint8_t vlds[kDecWaves][32 * 256];
@@ -91,32 +93,27 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   const int half = blockIdx.y;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int n = l & 15, b = l >> 4;  // MFMA column / k-group of this lane
-  if (a.prep.qw) {
-    // the QK producers on the half's 16 query heads: two per wave, one dim
-    // per lane, into LDS
-    float sn, cs;
-    rope_sincos(l, a.qpos, a.prep.rt, sn, cs);
-    const float wq = h2f(a.prep.qw[l]);
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-      const int hh = 2 * w + r;
-      qprep[hh * D + l] =
-          qk_norm_rope_sc(h2f(a.q[(size_t)(half * 16 + hh) * D + l]), wq, l, sn, cs, a.prep.eps);
-    }
-    __syncthreads();
-  }
   uint8_t* kw = klds[w];
   uint8_t* vw = vlds[w];
   // this wave's pairs: an even share of the half's pairs
   const int nwaves = a.nwg * kDecWaves;
   const int wid = blockIdx.x * kDecWaves + w;
-  const int p0 = (int)(((long long)wid * a.npairs) / nwaves);
-  const int p1 = (int)(((long long)(wid + 1) * a.npairs) / nwaves);
-  // Q^T as the block-diagonal B operand, fp16
+  // (wid * npairs < 2^31: at most 1024 waves per half, 2^21 pairs)
+  const int p0 = (int)(((unsigned)wid * (unsigned)a.npairs) / (unsigned)nwaves);
+  const int p1 = (int)(((unsigned)(wid + 1) * (unsigned)a.npairs) / (unsigned)nwaves);
+  // Q^T as the block-diagonal B operand, fp16.  Prepared q is loaded before
+  // the first pair; raw q (with the QK producers) is loaded first too, but
+  // normalised and rotated while the first pair's K/V loads are in flight.
   f16x8 qop[8];
-  if ((n >> 2) == b && a.prep.qw) {
+  // (32-bit holders: packing two loaded halves into one register would
+  // wait for both loads on the spot)
+  uint32_t qraw[2] = {0u, 0u}, wraw = 0u;
+  float invf = 0.0f;
+  if constexpr (kPrep) {
+    invf = a.prep.rt.invf[l & 31];
+    wraw = a.prep.qw[l];
 #pragma unroll
-    for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qprep + n * D + 8 * mu);
+    for (int r = 0; r < 2; r++) qraw[r] = a.q[(size_t)(half * 16 + 2 * w + r) * D + l];
   } else if ((n >> 2) == b) {
     const uint16_t* qp = a.q + (size_t)(half * 16 + n) * D;
 #pragma unroll
@@ -125,27 +122,63 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
 #pragma unroll
     for (int mu = 0; mu < 8; mu++) qop[mu] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
+  // loads of a pair: instruction i covers keys 4i..4i+3, lane -> (key 4i + b,
+  // chunk n); the group scales first, then all K, then all V, so S^T and the
+  // softmax run while V is still arriving
+  uint16_t ksc_h = 0, vsc_h = 0;
+  u32x4 kr[8], vr[8];
+  auto load_pair = [&](int p, const uint8_t* kc8, const uint8_t* vc8) {
+    const int kbase = p * 32, grp = kbase >> 6;
+    ksc_h = a.ksc[grp * NKV + half * 4 + (n >> 2)];
+    vsc_h = a.vsc[grp * NKV + half * 4 + b];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      kr[i] = *(const u32x4*)(kc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      vr[i] = *(const u32x4*)(vc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+  };
+  // The first pair is loaded without a branch (a wave without pairs reads
+  // pair 0, or with no committed pair at all the first 16 KiB of the tail
+  // buffers, and never uses the values), so the waits that follow count
+  // only this wave's own earlier loads.
+  {
+    const bool cache = p0 < p1 || a.npairs > 0;
+    load_pair(p0 < p1 ? p0 : 0, cache ? a.kc8 : (const uint8_t*)a.ktail,
+              cache ? a.vc8 : (const uint8_t*)a.vtail);
+  }
+  if constexpr (kPrep) {
+    // (keeps the producers' arithmetic behind the first pair's loads, so it
+    // waits only for its own older loads)
+    __builtin_amdgcn_sched_barrier(0);
+    // the QK producers on the half's 16 query heads: two per wave, one dim
+    // per lane, into LDS
+    float sn, cs;
+    rope_sincos_f(invf, a.qpos, sn, cs);
+    const float wq = h2f((uint16_t)wraw);
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+      qprep[(2 * w + r) * D + l] =
+          qk_norm_rope_sc(h2f((uint16_t)qraw[r]), wq, l, sn, cs, a.prep.eps);
+    // LDS writes done, then the barrier alone: a full __syncthreads would
+    // also wait for the first pair's K/V loads
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if ((n >> 2) == b) {
+#pragma unroll
+      for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qprep + n * D + 8 * mu);
+    } else {
+#pragma unroll
+      for (int mu = 0; mu < 8; mu++) qop[mu] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
   const float qscale = a.scale * kLog2e;
   float mx = -1e30f, lsum = 0.f;  // column (a, j) = n: running max (log2) and sum
   f32x4 O[4];                     // rows (kv head b, query head i), dims 16 nu + n
 #pragma unroll
   for (int v = 0; v < 4; v++) O[v] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p = p0; p < p1; p++) {
-    const int kbase = p * 32;
-    // ---- loads: instruction i covers keys 4i..4i+3, lane -> (key 4i + b, chunk n);
-    // all K first, so S^T and the softmax run while V is still arriving
-    // (the group scales are loaded first: waiting for them then waits for
-    // nothing else)
-    const int grp = kbase >> 6;
-    const uint16_t ksc_h = a.ksc[grp * NKV + half * 4 + (n >> 2)];
-    const uint16_t vsc_h = a.vsc[grp * NKV + half * 4 + b];
-    u32x4 kr[8], vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      kr[i] = *(const u32x4*)(a.kc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      vr[i] = *(const u32x4*)(a.vc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+    if (p != p0) load_pair(p, a.kc8, a.vc8);
     // K scale of this lane's column kv head (times scale*log2e), V scale of
     // this lane's row kv head
     const float ksc = h2f(ksc_h) * qscale;
@@ -265,24 +298,27 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
 // 8 items of a head -- and the 4 heads of one kv head -- share an XCD and
 // read that head's partials and tail rows through one L2.  Lane s holds FP8
 // partials s and s + 64; lane t attends tail key committed + t.
+template <bool kPrep>
 __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   const int j = blockIdx.x >> 3;
   const int h = (blockIdx.x & 7) * 4 + (j >> 3), c = j & 7, kvh = h / GQA;
   const int l = threadIdx.x;
   const int ntail = a.qpos + 1 - a.committed;  // 0..64
-  // the QK producers on this head's q row and the fresh k row (one dim per
-  // lane) when they arrive raw
+  // with the QK producers: this head's raw q row and the fresh raw k row
+  // (one dim per lane) are loaded first and prepared while the partials
+  // load
   __shared__ __attribute__((aligned(16))) uint16_t prep[2 * D];
-  const bool raw = a.prep.qw != nullptr;
-  if (raw) {
-    float sn, cs;
-    rope_sincos(l, a.qpos, a.prep.rt, sn, cs);
-    prep[l] = qk_norm_rope_sc(h2f(a.q[(size_t)h * D + l]), h2f(a.prep.qw[l]), l, sn, cs,
-                              a.prep.eps);
-    if (a.knew)
-      prep[D + l] = qk_norm_rope_sc(h2f(a.knew[(size_t)kvh * D + l]), h2f(a.prep.kw[l]), l, sn,
-                                    cs, a.prep.eps);
-    __syncthreads();
+  constexpr bool raw = kPrep;
+  uint32_t qraw = 0u, kraw = 0u, wq = 0u, wk = 0u;
+  float invf = 0.0f;
+  if constexpr (kPrep) {
+    invf = a.prep.rt.invf[l & 31];
+    qraw = a.q[(size_t)h * D + l];
+    wq = a.prep.qw[l];
+    if (a.knew) {
+      kraw = a.knew[(size_t)kvh * D + l];
+      wk = a.prep.kw[l];
+    }
   }
   const uint16_t* qrow = raw ? prep : a.q + (size_t)h * D;
   const uint16_t* knew = raw ? prep + D : (a.knew ? a.knew + (size_t)kvh * D : nullptr);
@@ -304,6 +340,18 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
       pl[u] = 0.f;
       po[u][0] = po[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+  if constexpr (kPrep) {
+    __builtin_amdgcn_sched_barrier(0);
+    float sn, cs;
+    rope_sincos_f(invf, a.qpos, sn, cs);
+    prep[l] = qk_norm_rope_sc(h2f((uint16_t)qraw), h2f((uint16_t)wq), l, sn, cs, a.prep.eps);
+    if (a.knew)
+      prep[D + l] =
+          qk_norm_rope_sc(h2f((uint16_t)kraw), h2f((uint16_t)wk), l, sn, cs, a.prep.eps);
+    // one wave: the LDS writes are complete once lgkmcnt reaches 0 (no
+    // barrier needed, no wait for the partials' loads)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
   }
   u32x4 kq[8], qq[8], vrow[8], vv = u32x4{0u, 0u, 0u, 0u};
   const bool live = l < ntail;
@@ -487,7 +535,10 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
                 (float*)ws, npairs, nwg, out, QkPrep{}};
   if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_decode_attend, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
+  if (da.prep.qw)
+    hipLaunchKernelGGL(k_decode_attend<true>, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
+  else
+    hipLaunchKernelGGL(k_decode_attend<false>, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
   int st = launch_status();
   if (st) return st;
   if (mid_event) {
@@ -497,6 +548,9 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
       return CIA_ERR_HIP;
     }
   }
-  hipLaunchKernelGGL(k_decode_finish, dim3(kItems), dim3(64), 0, s, da);
+  if (da.prep.qw)
+    hipLaunchKernelGGL(k_decode_finish<true>, dim3(kItems), dim3(64), 0, s, da);
+  else
+    hipLaunchKernelGGL(k_decode_finish<false>, dim3(kItems), dim3(64), 0, s, da);
   return launch_status();
 }

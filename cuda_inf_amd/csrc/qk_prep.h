@@ -4,7 +4,7 @@
 // single IEEE-rounded op in a fixed order, so the result is bit-identical
 // to the CPU restatement:
 //   ss  = sum of x^2 in the reference's tree order (pairs d, d + s for
-//         s = 32..1: the xor butterfly gives every lane that tree's sum)
+//         s = 32..1, lower + upper), broadcast from lane 0
 //   inv = 1 / sqrt(ss / 64 + eps)          (IEEE sqrt and division)
 //   y   = fp16((x * inv) * w)
 //   for d < 32: ang = pos * invf[d], (sn, cs) = sincos_det(ang),
@@ -54,11 +54,16 @@ __device__ __forceinline__ float fp32_round(float v) {
   return v;
 }
 
+// The rotation of frequency invf at position pos
+__device__ __forceinline__ void rope_sincos_f(float invf, int pos, float& sn, float& cs) {
+#pragma clang fp contract(off)
+  sincos_det((float)pos * invf, sn, cs);
+}
+
 // The rotation of lane d's frequency (d mod 32) at position pos
 __device__ __forceinline__ void rope_sincos(int d, int pos, const RopeTable& rt, float& sn,
                                             float& cs) {
-#pragma clang fp contract(off)
-  sincos_det((float)pos * rt.invf[d & 31], sn, cs);
+  rope_sincos_f(rt.invf[d & 31], pos, sn, cs);
 }
 
 // One head row, lane d holding x = row[d] and w = weight[d], (sn, cs) the
@@ -67,10 +72,13 @@ __device__ __forceinline__ void rope_sincos(int d, int pos, const RopeTable& rt,
 __device__ __forceinline__ uint16_t qk_norm_rope_sc(float x, float w, int d, float sn, float cs,
                                                     float eps) {
 #pragma clang fp contract(off)
-  const float ss = wave_sum(x * x);
+  const float ss = wave_tree_sum(x * x);
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
   const float y = h2f(f2h(fp32_round((x * inv) * w)));
-  const float other = __shfl_xor(y, 32);
+  // dim d ^ 32: the swap hands lanes below 32 their partner in the second
+  // register and lanes from 32 in the first
+  const f32x2 sw = swap32(y);
+  const float other = d < 32 ? sw[1] : sw[0];
   const float r = d < 32 ? y * cs - other * sn : y * cs + other * sn;
   return f2h(fp32_round(r));
 }
