@@ -45,6 +45,9 @@ SIGNATURES = {
     "cia_h2o_workspace_bytes": (ctypes.c_int64, [_I, _I]),
     "cia_mass_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_qk_norm_rope": (_I, [_P, _P, _P, _P, _P, _I, _F, _F, _P]),
+    "cia_gemv_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "cia_gemv_int4_add": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "cia_qkv_proj_int4": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P]),
     "cia_kv_append_plan": (_I, [_P, _I, _I, _P, _I, _P]),
     "cia_h2o_clamp": (None, [_P, _P, _I, _I]),
     "cia_h2o_pick_slots": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),

@@ -188,3 +188,31 @@ def qk_norm_rope(q, k, qw, kw, pos, S: int, eps: float = 1e-5, theta: float = 5.
     call("cia_qk_norm_rope", _dev(q, "q", _F16, S * NH * D), _dev(k, "k", _F16, S * NKV * D),
          _dev(qw, "qw", _F16, D), _dev(kw, "kw", _F16, D), _dev(pos, "pos", (torch.int32,), S),
          S, float(eps), float(theta), _stream())
+
+
+# ------------------------------------------------------------ INT4 projections
+def _int4(packed, scales, N: int, K: int, name: str):
+    return (_dev(packed, name + ".packed", (torch.uint8,), N * K // 2),
+            _dev(scales, name + ".scales", _F16, N * K // 128))
+
+
+def gemv_int4(x, packed, scales, y, N: int, K: int, M: int, add: bool = False) -> None:
+    """engine.cu:83-109 / 626-630: y fp32 [M, N] = x [M, K] W^T for INT4
+    group-128 W (packed u8 [N, K/2], scales fp16 [N, K/128]); add=True
+    accumulates into y (out_proj + residual, engine.cu:858-859)."""
+    p, s = _int4(packed, scales, N, K, "w")
+    call("cia_gemv_int4_add" if add else "cia_gemv_int4", _dev(x, "x", _F16, M * K), p, s,
+         _dev(y, "y", (torch.float32,), M * N), N, K, M, _stream())
+
+
+def qkv_proj_int4(x, wq, wk, wv, q, k, v, M: int, K: int = 2048) -> None:
+    """engine.cu:792-797 in one launch: q/k/v fp16 = fp16(x W^T); wq, wk, wv
+    are (packed, scales) pairs with N = q.shape[-1] / k.shape[-1] rows."""
+    Nq = q.numel() // M
+    Nkv = k.numel() // M
+    pq, sq = _int4(*wq, Nq, K, "wq")
+    pk, sk = _int4(*wk, Nkv, K, "wk")
+    pv, sv = _int4(*wv, Nkv, K, "wv")
+    call("cia_qkv_proj_int4", _dev(x, "x", _F16, M * K), pq, sq, Nq, pk, sk, pv, sv, Nkv, K, M,
+         _dev(q, "q", _F16, M * Nq), _dev(k, "k", _F16, M * Nkv), _dev(v, "v", _F16, M * Nkv),
+         _stream())

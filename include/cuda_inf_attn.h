@@ -230,6 +230,39 @@ int cia_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* qw,
                      float theta, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* INT4 group-128 projections                                         */
+/* ------------------------------------------------------------------ */
+/* Weight format of tools/export_weights.py:7-13, 64-79 (the Q4 views of
+ * engine.cu:58, 65-71): W [N][K] as packed u8 [N][K/2] (two K-adjacent
+ * nibbles per byte, k even in the low nibble) followed by scales fp16
+ * [N][K/128]; w[n][k] = (nibble - 8) * scale[n][k/128].  K must be a
+ * positive multiple of 128; packed and x 16-byte aligned, scales 2-byte
+ * aligned.  Sums are fp32 (order differs from the reference's lanes). */
+
+/* gemv_int4 (engine.cu:83-109) as launched by run_gemv_int4
+ * (engine.cu:626-630): y[m][n] = sum_k x[m][k] * w[n][k] for m < M, n < N;
+ * x fp16 [M][K], y fp32 [M][N].  M = 0 is a no-op. */
+int cia_gemv_int4(const uint16_t* x, const uint8_t* packed,
+                  const uint16_t* scales, float* y, int N, int K, int M,
+                  void* stream);
+/* out_proj and the residual add (engine.cu:858-859, run_gemv_int4 then
+ * add_f32_inplace): y[m][n] += sum_k x[m][k] * w[n][k], one launch. */
+int cia_gemv_int4_add(const uint16_t* x, const uint8_t* packed,
+                      const uint16_t* scales, float* y, int N, int K, int M,
+                      void* stream);
+/* The q, k and v projections of an attention layer with their fp16
+ * conversions (engine.cu:792-797: three run_gemv_int4 and three f32_to_f16)
+ * in one launch: q fp16 [M][Nq] = fp16(x Wq^T), k, v fp16 [M][Nkv]; each
+ * output is the round-to-nearest-even fp16 of its fp32 sum, as f32_to_f16
+ * makes it. */
+int cia_qkv_proj_int4(const uint16_t* x, const uint8_t* wq_packed,
+                      const uint16_t* wq_scales, int Nq,
+                      const uint8_t* wk_packed, const uint16_t* wk_scales,
+                      const uint8_t* wv_packed, const uint16_t* wv_scales,
+                      int Nkv, int K, int M, uint16_t* q, uint16_t* k,
+                      uint16_t* v, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* host-side policy (plain C++, no device access)                     */
 /* ------------------------------------------------------------------ */
 

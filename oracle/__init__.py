@@ -72,6 +72,8 @@ def _declare(L):
         "orc_kv_quant_write": (None, [_P] * 7 + [_I]),
         "orc_attention_h2o": (None, [_P] * 6 + [_I, _P, _P, _P, _I, _I, _F]),
         "orc_h2o_pick_slots": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),
+        "orc_quant_int4_g128": (None, [_P, _I, _I, _P, _P]),
+        "orc_gemv_int4": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -303,3 +305,32 @@ def h2o_pick_slots(n_live, C, W, slotpos, attn_host, S, past):
     ev = lib().orc_h2o_pick_slots(ctypes.byref(nl), C, W, _p(slotpos), _p(attn_host), S, past,
                                   _p(dst), _p(zeroed))
     return nl.value, dst, zeroed, ev
+
+
+# ---------------------------------------------------------------- INT4 g128
+def quant_int4_g128(w):
+    """tools/export_weights.py:64-79: fp32 [N, K] -> (packed u8 [N, K/2],
+    scales fp16 bits [N, K/128])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    assert K % 128 == 0
+    packed = np.zeros((N, K // 2), np.uint8)
+    scales = np.zeros((N, K // 128), np.uint16)
+    lib().orc_quant_int4_g128(_p(w), N, K, _p(packed), _p(scales))
+    return packed, scales
+
+
+def gemv_int4(x, packed, scales, want_absum: bool = False):
+    """engine.cu:83-109: x fp16 [M, K] -> y fp32 [M, N] (fp64 accumulation)."""
+    x = np.ascontiguousarray(_u16(x), dtype=np.uint16)
+    if x.ndim == 1:
+        x = x[None, :]
+    M, K = x.shape
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(_u16(scales), dtype=np.uint16)
+    N = packed.shape[0]
+    assert packed.shape == (N, K // 2) and scales.shape == (N, K // 128)
+    y = np.zeros((M, N), np.float32)
+    ab = np.zeros((M, N), np.float32) if want_absum else None
+    lib().orc_gemv_int4(_p(x), _p(packed), _p(scales), _p(y), _p(ab), N, K, M)
+    return (y, ab) if want_absum else y

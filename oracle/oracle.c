@@ -44,6 +44,17 @@
  *                         2.6e5), exact values at 0, odd/even symmetry bit
  *                         for bit, sin^2 + cos^2 = 1.
  *   rope_invf             float32 rounding of float64 theta^(-2i/64).
+ *   quant_int4_g128       closed forms: a group of amax 7 (scale 1) with
+ *                         ties at +-0.5, 1.5, 2.5 (half-to-even), a zero
+ *                         group (scale 0, nibbles 8), one non-zero element
+ *                         placed at even / odd k and in each group (nibble
+ *                         order, group index); |w - dequant| <= scale/2 and
+ *                         the amax element at nibble 1 or 15 on random
+ *                         weights.
+ *   gemv_int4             an independent numpy fp64 product of the
+ *                         dequantised dense matrix; one-hot x gives a
+ *                         dequantised column exactly; constant nibbles give
+ *                         scale * sum(x).
  *   qk_norm_rope          an independent numpy float32 restatement of the
  *                         norm (tree-ordered sum of squares) and rotation;
  *                         unit-RMS rows, pair norms kept, position 0 is the
@@ -734,4 +745,55 @@ int orc_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos,
     dst[j] = slot;
   }
   return evictions;
+}
+
+/* tools/export_weights.py:64-79 */
+void orc_quant_int4_g128(const float* w, int N, int K, uint8_t* packed, uint16_t* scales) {
+  const int ng = K / 128;
+  for (int n = 0; n < N; n++)
+    for (int g = 0; g < ng; g++) {
+      const float* wg = w + (size_t)n * K + (size_t)g * 128;
+      float amax = 0.0f;
+      for (int i = 0; i < 128; i++) {
+        const float a = fabsf(wg[i]);
+        if (a > amax) amax = a;
+      }
+      const float scale = amax / 7.0f;
+      const float safe = scale == 0.0f ? 1.0f : scale;
+      scales[(size_t)n * ng + g] = orc_f32_to_f16(scale);
+      uint8_t* pr = packed + (size_t)n * (K / 2) + (size_t)g * 64;
+      for (int i = 0; i < 128; i += 2) {
+        int nib[2];
+        for (int e = 0; e < 2; e++) {
+          float qv = rintf(wg[i + e] / safe); /* ties to even */
+          if (qv < -7.0f) qv = -7.0f;
+          if (qv > 7.0f) qv = 7.0f;
+          nib[e] = (int)qv + 8;
+        }
+        pr[i / 2] = (uint8_t)(nib[0] | (nib[1] << 4));
+      }
+    }
+}
+
+/* engine.cu:83-109 */
+void orc_gemv_int4(const uint16_t* x, const uint8_t* packed, const uint16_t* scales, float* y,
+                   float* absum, int N, int K, int M) {
+  const int ng = K / 128;
+  for (int m = 0; m < M; m++)
+    for (int n = 0; n < N; n++) {
+      const uint8_t* pr = packed + (size_t)n * (K / 2);
+      const uint16_t* sr = scales + (size_t)n * ng;
+      const uint16_t* xr = x + (size_t)m * K;
+      double acc = 0.0, aab = 0.0;
+      for (int k = 0; k < K; k++) {
+        const uint8_t b = pr[k >> 1];
+        const int nib = (k & 1) ? (b >> 4) : (b & 0xF);
+        const double wv = (double)(nib - 8) * (double)orc_f16_to_f32(sr[k >> 7]);
+        const double t = (double)orc_f16_to_f32(xr[k]) * wv;
+        acc += t;
+        aab += fabs(t);
+      }
+      y[(size_t)m * N + n] = (float)acc;
+      if (absum) absum[(size_t)m * N + n] = (float)aab;
+    }
 }

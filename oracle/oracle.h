@@ -152,6 +152,26 @@ int orc_h2o_pick_slots(int* n_live, int C, int W, int32_t* slotpos,
                        float* attn_sum_host, int S, int past, int32_t* dst,
                        int32_t* zeroed);
 
+/* ---- INT4 group-128 projections ------------------------------------ */
+/* The weight format of tools/export_weights.py:7-13, 64-79: W fp32 [N][K]
+ * (K a multiple of 128) -> packed u8 [N][K/2] (k even in the low nibble,
+ * nibble = q + 8) and scales fp16 [N][K/128].  Per group: amax = max |w|,
+ * scale = amax / 7 (fp32 division), q = round-half-even(w / scale') with
+ * scale' = scale or 1 when scale is 0, clipped to [-7, 7]; the stored
+ * scale is fp16(scale). */
+void orc_quant_int4_g128(const float* w, int N, int K, uint8_t* packed,
+                         uint16_t* scales);
+/* engine.cu:83-109 (gemv_int4, launched per row block by run_gemv_int4,
+ * 626-630): y[m][n] = sum_k x[m][k] * (nib(n,k) - 8) * scale[n][k/128],
+ * x fp16 [M][K], y fp32 [M][N].  The reference sums in fp32 in its lane
+ * order; this restatement sums the exact products in fp64 (the value the
+ * reference's sum approximates) and rounds once.  absum (may be NULL)
+ * receives sum_k |x * w| in fp64 rounded to fp32, the scale of the
+ * summation error. */
+void orc_gemv_int4(const uint16_t* x, const uint8_t* packed,
+                   const uint16_t* scales, float* y, float* absum, int N, int K,
+                   int M);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,16 @@ FAKE = 0x10000  # aligned non-null address: validation must fail before any use
     (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 5, FAKE, None, 1, 0, 0.125, FAKE, 1 << 20, None), 1),
     (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 100, FAKE, FAKE, 1, 0, 0.125, FAKE, 64, None), 3),
     (lambda L: L.cia_h2o_place(*([FAKE] * 9), None, 8, 2, 1, 0, None), 1),
+    (lambda L: L.cia_gemv_int4(FAKE, FAKE, FAKE, FAKE, 64, 100, 1, None), 3),    # K % 128
+    (lambda L: L.cia_gemv_int4(FAKE, FAKE, FAKE, FAKE, 0, 128, 1, None), 3),
+    (lambda L: L.cia_gemv_int4(None, None, None, None, 64, 128, 0, None), 0),     # M = 0
+    (lambda L: L.cia_gemv_int4(FAKE, None, FAKE, FAKE, 64, 128, 1, None), 1),
+    (lambda L: L.cia_gemv_int4(FAKE, FAKE + 8, FAKE, FAKE, 64, 128, 1, None), 2),
+    (lambda L: L.cia_gemv_int4_add(FAKE + 2, FAKE, FAKE, FAKE, 64, 128, 1, None), 2),
+    (lambda L: L.cia_qkv_proj_int4(FAKE, FAKE, FAKE, 64, FAKE, FAKE, FAKE, FAKE, 0, 128, 1,
+                                   FAKE, FAKE, FAKE, None), 3),
+    (lambda L: L.cia_qkv_proj_int4(FAKE, FAKE, FAKE, 64, FAKE, FAKE, FAKE, FAKE, 16, 128, 1,
+                                   FAKE, None, FAKE, None), 1),
     (lambda L: L.cia_e4m3_encode_range(0, -1, FAKE, None), 3),
     (lambda L: L.cia_e4m3_encode_range(0, 16, FAKE + 8, None), 2),
 ])
