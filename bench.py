@@ -67,6 +67,9 @@ def main():
     ap.add_argument("--prep-steps", type=int, default=64,
                     help="decode tokens with the QK producers run inside the decode kernels "
                          "(raw q/k in; 0 = skip)")
+    ap.add_argument("--block-steps", type=int, default=64,
+                    help="decode tokens through the whole attention branch: INT4 q/k/v "
+                         "projections, producers, attention, out_proj + residual (0 = skip)")
     ap.add_argument("--h2o-steps", type=int, default=4000,
                     help="H2O decode steps after a 1024-token prompt (0 = skip)")
     ap.add_argument("--calib-copy", type=int, default=0,
@@ -86,7 +89,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
-    total_steps = W + 2 * K + a.cold_steps + a.prep_steps
+    total_steps = W + 2 * K + a.cold_steps + a.prep_steps + a.block_steps
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
@@ -237,6 +240,78 @@ def main():
         log(f"decode with fused QK producers: {prep_us:.2f} us/token "
             f"({prep_us - us_tok:+.2f} against prepared inputs)")
 
+    # ---- the whole attention branch (engine.cu:792-859): INT4 q/k/v in one
+    # launch, producers + attention, out_proj into the residual; synthetic
+    # INT4 weights (uniform nibbles, scales 0.002-0.02)
+    block = None
+    if a.block_steps > 0:
+        gb = torch.Generator(device=dev)
+        gb.manual_seed(23)
+        H = _lib.HIDDEN
+        g8 = workload.generator(17, dev)
+        qw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        kw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        keep, parr = [], (_lib.cia_attn_proj * nL)()
+        for l in range(nL):
+            arr[l].qw, arr[l].kw = qw.data_ptr(), kw.data_ptr()
+            arr[l].eps, arr[l].theta = workload.EPS, workload.ROPE_THETA
+            pw = torch.zeros((NH + NKV) * D, dtype=torch.float16, device=dev)
+            arr[l].prep_ws, arr[l].prep_cap = pw.data_ptr(), 1
+            keep.append(pw)
+            for name, N in (("q", NH * D), ("k", NKV * D), ("v", NKV * D), ("o", H)):
+                pk = torch.randint(0, 256, (N, H // 2), generator=gb, device=dev, dtype=torch.uint8)
+                sc = (0.002 + 0.018 * torch.rand((N, H // 128), generator=gb, device=dev)).half()
+                setattr(parr[l], name + "_packed", pk.data_ptr())
+                setattr(parr[l], name + "_scales", sc.data_ptr())
+                keep += [pk, sc]
+            ws = torch.zeros(2 * NH * D + 2 * NKV * D, dtype=torch.float16, device=dev)
+            parr[l].ws, parr[l].cap = ws.data_ptr(), 1
+            keep.append(ws)
+        nb = a.block_steps
+        xb = torch.randn((nb, nL, H), generator=gb, device=dev).half()
+        hb = torch.zeros(H, dtype=torch.float32, device=dev)
+
+        def run_block(i0, n, events=None):
+            call("cia_attn_block_loop", arr, parr, nL, xb.data_ptr() + i0 * nL * H * 2,
+                 hb.data_ptr(), ctx + cur["step"], n, 0.125, events, stream.cuda_stream)
+            cur["step"] += n
+
+        n_ev = 4
+        n_t = nb - 2 - n_ev
+        run_block(0, 2)
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        run_block(2, n_t)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        blk_us = c0.elapsed_time(c1) * 1e3 / n_t
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(4 * n_ev * nL)]
+        for e in evs:  # the hipEvent_t handles exist once recorded
+            e.record(stream)
+        torch.cuda.synchronize()
+        run_block(2 + n_t, n_ev, (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs]))
+        torch.cuda.synchronize()
+        parts = [[], [], []]
+        for r in range(n_ev * nL):
+            for j in range(3):
+                parts[j].append(evs[4 * r + j].elapsed_time(evs[4 * r + j + 1]) * 1e3)
+        med = [sorted(p)[len(p) // 2] for p in parts]
+        for l in range(nL):
+            arr[l].qw = arr[l].kw = arr[l].prep_ws = None
+            arr[l].prep_cap = 0
+        wbytes = (2 * NH * D + 2 * NKV * D) * (H // 2 + H // 64)
+        block = {"us_per_token": round(blk_us, 2), "tokens": n_t,
+                 "us_per_layer": round(blk_us / nL, 2),
+                 "event_bracketed_us": {"qkv_proj": round(med[0], 2), "attention": round(med[1], 2),
+                                        "out_proj_residual": round(med[2], 2)},
+                 "int4_weight_bytes_per_layer": wbytes,
+                 "launches_per_layer": 4,
+                 "kernels": "k_gemv_int4 (q/k/v), k_decode_attend + k_decode_finish "
+                            "(producers inside), k_gemv_int4 (out_proj + residual)"}
+        log(f"attention branch (INT4 projections + attention): {blk_us:.2f} us/token; "
+            f"per layer qkv {med[0]:.2f} / attention {med[1]:.2f} / out_proj {med[2]:.2f} us")
+
     # ---- prefill leg: causal attention_fused over a fresh cache
     prefill = None
     if a.prefill > 0:
@@ -349,6 +424,7 @@ def main():
                                             "k_decode_finish": round(fin_us, 3)}},
         "prefill": prefill,
         "qk_producers_fused": prep,
+        "attention_branch": block,
         "long_context": long_ctx,
         "h2o": h2o,
         "cpu_baseline": cpu,

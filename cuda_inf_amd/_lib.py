@@ -17,6 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 # Shapes (engine.cu:22-23, 35-38)
 NH, NKV, GQA, D, KVGROUP = 32, 8, 4, 64, 64
 NSPLIT_DEFAULT = 16
+HIDDEN = 2048  # hidden size H (engine.cu:33)
 NSPLIT_MAX = 4096
 
 STATUS = {0: "CIA_OK", 1: "CIA_ERR_NULL", 2: "CIA_ERR_ALIGN", 3: "CIA_ERR_ARG",
@@ -48,6 +49,8 @@ SIGNATURES = {
     "cia_gemv_int4": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "cia_gemv_int4_add": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "cia_qkv_proj_int4": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P]),
+    "cia_attn_block_forward": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_attn_block_loop": (_I, [_P, _P, _I, _P, _P, _I, _I, _F, _P, _P]),
     "cia_kv_append_plan": (_I, [_P, _I, _I, _P, _I, _P]),
     "cia_h2o_clamp": (None, [_P, _P, _I, _I]),
     "cia_h2o_pick_slots": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),
@@ -108,6 +111,15 @@ def call(fn: str, *args) -> None:
 class cia_append_op(ctypes.Structure):
     _fields_ = [("src_token", _I), ("slot", _I), ("cnt", _I), ("commit", _I),
                 ("commit_base", _I), ("commit_grp", _I)]
+
+
+class cia_attn_proj(ctypes.Structure):
+    """Mirror of ``cia_attn_proj`` in include/cuda_inf_attn.h."""
+    _fields_ = [
+        ("q_packed", _P), ("q_scales", _P), ("k_packed", _P), ("k_scales", _P),
+        ("v_packed", _P), ("v_scales", _P), ("o_packed", _P), ("o_scales", _P),
+        ("ws", _P), ("cap", _I),
+    ]
 
 
 class cia_layer(ctypes.Structure):

@@ -41,6 +41,7 @@ struct GemvArgs {
 };
 
 constexpr int kGemvWaves = 8;
+constexpr int kGemmMinM = 80;  // rows of x from which the matrix-core GEMM runs (measured crossover)
 
 // nibbles sh..sh+3 and sh+16..sh+19 of w as fp16 (nibble - 8), exact
 __device__ __forceinline__ f16x2 nib_pair(uint32_t w, int sh) {
@@ -182,6 +183,173 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv_int4(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- GEMM
+// Many rows of x (prefill): Y = X W^T on the fp16 matrix cores
+// (v_mfma_f32_16x16x32_f16).  A workgroup computes a 128 (x rows) x 128
+// (weight rows) tile with 4 waves in a 2 x 2 grid of 64 x 64 wave tiles
+// (4 x 4 MFMA tiles).  The K loop runs over the 128-wide scale groups: the
+// products of one group accumulate from zero on the matrix cores and are
+// then added with the group scale of their column in fp32, so the weights
+// enter the MFMA as exact fp16 (nibble - 8) values.
+//   Inside a group the k order of the four 32-k MFMA steps is permuted the
+//   same way for both operands: lane group q = l >> 4 holds k = 32q + 8s ..
+//   32q + 8s + 7 at step s.  So one 16-byte load per lane and column tile
+//   brings the nibbles of all four steps (k = 32q .. 32q+31), word s being
+//   step s.
+//   X tiles go through LDS (two buffers, 32 KiB each): row r, 16-byte chunk
+//   c at chunk c ^ (r & 15), so the 16 rows of an MFMA read hit distinct
+//   banks.  The next group's X and weights are loaded while this group
+//   computes; one barrier per group.
+constexpr int kTile = 128;
+
+// 8 nibbles (one u32, k even in the low nibble) -> 8 fp16 (nibble - 8), in k order
+__device__ __forceinline__ f16x8 nib8(uint32_t u) {
+  const uint32_t x = u & 0x0F0F0F0Fu, y = (u >> 4) & 0x0F0F0F0Fu;
+  const f16x2 off = f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
+  f16x8 r;
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    // {lo_b, hi_b} as 16-bit values, then under the exponent of 1024
+    const uint32_t sel = 0x0C000C00u | (uint32_t)(4 + b) << 16 | (uint32_t)b;
+    const f16x2 h =
+        __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(y, x, sel) | 0x64006400u) - off;
+    r[2 * b] = h[0];
+    r[2 * b + 1] = h[1];
+  }
+  return r;
+}
+
+// grid = (ceil(rows / 128), ceil(M / 128)), block = 256
+__global__ __launch_bounds__(256) void k_gemm_int4(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kTile * 128];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int wm = w >> 1, wn = w & 1, n16 = l & 15, q = l >> 4;
+  const int m0 = blockIdx.y * kTile, r0 = blockIdx.x * kTile;
+  const int K = a.K, ng = K >> 7;
+  // this lane's weight row in each of the wave's 4 column tiles
+  const uint8_t* wrow[4];
+  const uint16_t* srow[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    int n = r0 + 64 * wn + 16 * j + n16;
+    n = n < a.rows ? n : a.rows - 1;
+    int mi = 0;
+    if (n >= a.mat[0].N) {
+      n -= a.mat[0].N;
+      mi = 1;
+      if (n >= a.mat[1].N) {
+        n -= a.mat[1].N;
+        mi = 2;
+      }
+    }
+    const uint8_t* pk = mi == 0 ? a.mat[0].packed : (mi == 1 ? a.mat[1].packed : a.mat[2].packed);
+    const uint16_t* sc = mi == 0 ? a.mat[0].scales : (mi == 1 ? a.mat[1].scales : a.mat[2].scales);
+    wrow[j] = pk + (size_t)n * (K >> 1) + 16 * q;
+    srow[j] = sc + (size_t)n * ng;
+  }
+  // X staging: pass p moves rows 16p + (tid >> 4), chunk tid & 15
+  const int sr = tid >> 4, sc16 = tid & 15;
+  const uint16_t* xrow[8];
+#pragma unroll
+  for (int p = 0; p < 8; p++) {
+    const int m = m0 + 16 * p + sr;
+    xrow[p] = a.x + (size_t)(m < a.M ? m : a.M - 1) * K + 8 * sc16;
+  }
+  const int xdst = sr * 128 + 8 * (sc16 ^ (sr & 15));  // + 16 * 128 * p
+  u32x4 xv[8], wv[4];
+  uint32_t sv[4];
+  auto load = [&](int g) {
+#pragma unroll
+    for (int p = 0; p < 8; p++) xv[p] = *(const u32x4*)(xrow[p] + 128 * g);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      wv[j] = *(const u32x4*)(wrow[j] + 64 * g);
+      sv[j] = srow[j][g];
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 8; p++) *(u32x4*)(&xs[buf][16 * 128 * p + xdst]) = xv[p];
+  };
+  f32x4 C[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) C[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  stage(0);
+  __syncthreads();
+  for (int g = 0; g < ng; g++) {
+    const int buf = g & 1;
+    u32x4 wc[4];
+    float scl[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      wc[j] = wv[j];
+      scl[j] = h2f((uint16_t)sv[j]);
+    }
+    if (g + 1 < ng) load(g + 1);
+    f32x4 P[4][4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      f16x8 A[4], B[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = 64 * wm + 16 * i + n16;
+        A[i] = *(const f16x8*)(&xs[buf][r * 128 + 8 * ((4 * q + s) ^ n16)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) B[j] = nib8(wc[j][s]);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              A[i], B[j], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[i][j], 0, 0, 0);
+    }
+    // C += P * scale of the column (the lane's column is n16 of tile j)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) C[i][j][e] = __builtin_fmaf(P[i][j][e], scl[j], C[i][j][e]);
+    if (g + 1 < ng) {
+      stage(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  // outputs: lane holds rows 4q + e of tile i, column n16 of tile j
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int col = r0 + 64 * wn + 16 * j + n16;
+    if (col >= a.rows) continue;
+    int n = col, mi = 0;
+    if (n >= a.mat[0].N) {
+      n -= a.mat[0].N;
+      mi = 1;
+      if (n >= a.mat[1].N) {
+        n -= a.mat[1].N;
+        mi = 2;
+      }
+    }
+    float* y32 = mi == 0 ? a.mat[0].y32 : (mi == 1 ? a.mat[1].y32 : a.mat[2].y32);
+    uint16_t* y16 = mi == 0 ? a.mat[0].y16 : (mi == 1 ? a.mat[1].y16 : a.mat[2].y16);
+    const int N = mi == 0 ? a.mat[0].N : (mi == 1 ? a.mat[1].N : a.mat[2].N);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int m = m0 + 64 * wm + 16 * i + 4 * q + e;
+        if (m >= a.M) continue;
+        const size_t o = (size_t)m * N + n;
+        const float v = C[i][j][e];
+        if (y32) y32[o] = a.add ? y32[o] + v : v;
+        if (y16) y16[o] = f2h(v);
+      }
+  }
+}
+
 template <int kM>
 static void gemv_launch(const GemvArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.rows + kGemvWaves - 1) / kGemvWaves),
@@ -201,7 +369,10 @@ static void gemv_launch(const GemvArgs& a, hipStream_t s) {
 static int gemv_run(GemvArgs& a, void* stream) {
   a.rows = a.mat[0].N + a.mat[1].N + a.mat[2].N;
   hipStream_t s = (hipStream_t)stream;
-  if (a.M == 1)
+  if (a.M >= kGemmMinM) {
+    hipLaunchKernelGGL(k_gemm_int4, dim3((unsigned)((a.rows + kTile - 1) / kTile),
+                       (unsigned)((a.M + kTile - 1) / kTile)), dim3(256), 0, s, a);
+  } else if (a.M == 1)
     gemv_launch<1>(a, s);
   else if (a.M == 2)
     gemv_launch<2>(a, s);

@@ -339,3 +339,64 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
   }
   return CIA_OK;
 }
+
+// ---------------------------------------------------------------- attention branch
+static int proj_check(const cia_attn_proj* P) {
+  if (!P || !P->q_packed || !P->q_scales || !P->k_packed || !P->k_scales || !P->v_packed ||
+      !P->v_scales || !P->o_packed || !P->o_scales || !P->ws)
+    return CIA_ERR_NULL;
+  if (P->cap < 1) return CIA_ERR_ARG;
+  return CIA_OK;
+}
+
+// engine.cu:792-859 for S tokens; ev (may be NULL) = 4 events as documented
+static int attn_block(cia_layer* L, const cia_attn_proj* P, const uint16_t* x, float* h, int S,
+                      int past, float scale, int* evicted, void* stream, void* const* ev) {
+  constexpr int H = CIA_HIDDEN, NQ = CIA_NH * CIA_HEAD_DIM, NK = CIA_NKV * CIA_HEAD_DIM;
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* q = P->ws;
+  uint16_t* k = q + (size_t)S * NQ;
+  uint16_t* v = k + (size_t)S * NK;
+  uint16_t* o = v + (size_t)S * NK;
+  int st;
+  if (ev && (st = hip_check(hipEventRecord((hipEvent_t)ev[0], s)))) return st;
+  if ((st = cia_qkv_proj_int4(x, P->q_packed, P->q_scales, NQ, P->k_packed, P->k_scales,
+                              P->v_packed, P->v_scales, NK, H, S, q, k, v, stream)))
+    return st;
+  if (ev && (st = hip_check(hipEventRecord((hipEvent_t)ev[1], s)))) return st;
+  if ((st = cia_layer_forward(L, q, k, v, o, S, past, scale, evicted, stream))) return st;
+  if (ev && (st = hip_check(hipEventRecord((hipEvent_t)ev[2], s)))) return st;
+  if ((st = cia_gemv_int4_add(o, P->o_packed, P->o_scales, h, H, NQ, S, stream))) return st;
+  if (ev && (st = hip_check(hipEventRecord((hipEvent_t)ev[3], s)))) return st;
+  return CIA_OK;
+}
+
+extern "C" int cia_attn_block_forward(cia_layer* L, const cia_attn_proj* P, const uint16_t* x,
+                                      float* h, int S, int past, float scale, int* evicted,
+                                      void* stream) {
+  if (!L || !x || !h) return CIA_ERR_NULL;
+  int st = proj_check(P);
+  if (st) return st;
+  if (S < 1 || past < 0 || S > P->cap) return CIA_ERR_ARG;
+  return attn_block(L, P, x, h, S, past, scale, evicted, stream, nullptr);
+}
+
+extern "C" int cia_attn_block_loop(cia_layer* layers, const cia_attn_proj* proj, int n_layers,
+                                   const uint16_t* x, float* h, int past, int steps, float scale,
+                                   void** events, void* stream) {
+  if (!layers || !proj || !x || !h) return CIA_ERR_NULL;
+  if (n_layers < 1 || steps < 0 || past < 0) return CIA_ERR_ARG;
+  for (int l = 0; l < n_layers; l++) {
+    int st = proj_check(&proj[l]);
+    if (st) return st;
+    if ((st = prep_check(&layers[l]))) return st;
+  }
+  for (int i = 0; i < steps; i++)
+    for (int l = 0; l < n_layers; l++) {
+      const size_t r = (size_t)i * n_layers + l;
+      const int st = attn_block(&layers[l], &proj[l], x + r * CIA_HIDDEN, h, 1, past + i, scale,
+                                nullptr, stream, events ? events + 4 * r : nullptr);
+      if (st) return st;
+    }
+  return CIA_OK;
+}

@@ -13,8 +13,11 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import D, KVGROUP, NH, NKV, NSPLIT_DEFAULT, call, cia_append_op, cia_layer
+from ._lib import (D, KVGROUP, NH, NKV, NSPLIT_DEFAULT, call, cia_append_op, cia_attn_proj,
+                   cia_layer)
 from .kernels import decode_workspace_bytes, h2o_workspace_bytes
+
+HIDDEN = _lib.HIDDEN
 
 
 # ------------------------------------------------------------ host policy
@@ -150,3 +153,63 @@ class AttnLayer:
              out.data_ptr(), S, past, float(scale), ctypes.byref(ev) if evicted else None,
              torch.cuda.current_stream().cuda_stream)
         return out, (ev.value if evicted else None)
+
+    # -------------------------------------------------------- projections
+    def set_projections(self, wq, wk, wv, wo):
+        """INT4 group-128 weights of q/k/v/out_proj (engine.cu:792-797, 858):
+        each a (packed u8 [N, 1024], scales fp16 [N, 16]) pair of device
+        tensors, N = 2048 / 512 / 512 / 2048."""
+        P = cia_attn_proj()
+        self._proj_w = []
+        for name, (pk, sc), N in (("q", wq, NH * D), ("k", wk, NKV * D), ("v", wv, NKV * D),
+                                  ("o", wo, HIDDEN)):
+            if (pk.dtype != torch.uint8 or not pk.is_cuda or not pk.is_contiguous()
+                    or pk.numel() != N * HIDDEN // 2):
+                raise ValueError(f"{name}_proj packed: need contiguous device uint8 [{N}, {HIDDEN // 2}]")
+            if (sc.dtype not in (torch.float16, torch.int16) or not sc.is_cuda
+                    or not sc.is_contiguous() or sc.numel() != N * HIDDEN // 128):
+                raise ValueError(f"{name}_proj scales: need contiguous device fp16 [{N}, {HIDDEN // 128}]")
+            setattr(P, name + "_packed", pk.data_ptr())
+            setattr(P, name + "_scales", sc.data_ptr())
+            self._proj_w += [pk, sc]
+        self.proj_ws = torch.zeros(self.max_batch * (2 * NH * D + 2 * NKV * D), dtype=torch.float16,
+                                   device=self.device)
+        P.ws, P.cap = self.proj_ws.data_ptr(), self.max_batch
+        self._p = P
+
+    def block_forward(self, x, h, past: int, scale: float = 0.125, evicted: bool = True):
+        """engine.cu:792-859: x fp16 [S, 2048] (normalised hidden state) through
+        q/k/v_proj, the QK producers (when the layer has qk_norm), attention
+        and out_proj, added into the residual h fp32 [S, 2048] in place.
+        Returns the evicted slot of the last token on an H2O layer (or -1;
+        None with evicted=False)."""
+        S = x.numel() // HIDDEN
+        if x.dtype != torch.float16 or not x.is_cuda or not x.is_contiguous() or x.numel() != S * HIDDEN:
+            raise ValueError("x: need a contiguous device fp16 tensor [S, 2048]")
+        if h.dtype != torch.float32 or not h.is_cuda or not h.is_contiguous() or h.numel() != S * HIDDEN:
+            raise ValueError("h: need a contiguous device fp32 tensor [S, 2048]")
+        ev = ctypes.c_int(-1)
+        call("cia_attn_block_forward", ctypes.byref(self._s), ctypes.byref(self._p), x.data_ptr(),
+             h.data_ptr(), S, past, float(scale), ctypes.byref(ev) if evicted else None,
+             torch.cuda.current_stream().cuda_stream)
+        return ev.value if evicted else None
+
+
+def attn_block_loop(layers, x, h, past: int, steps: int, scale: float = 0.125, events=None):
+    """cia_attn_block_loop: steps decode steps through the attention branches
+    of ``layers`` (AttnLayer with projections).  x fp16 [steps, n_layers, 2048],
+    h fp32 [2048] (the residual stream, added into in place)."""
+    n = len(layers)
+    arr = (cia_layer * n)(*[L._s for L in layers])
+    parr = (cia_attn_proj * n)(*[L._p for L in layers])
+    ev = None
+    if events is not None:
+        for e in events:  # the hipEvent_t handles exist once recorded
+            e.record()
+        ev = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+    try:
+        call("cia_attn_block_loop", arr, parr, n, x.data_ptr(), h.data_ptr(), past, steps,
+             float(scale), ev, torch.cuda.current_stream().cuda_stream)
+    finally:
+        for L, s in zip(layers, arr):  # host counters advance in the copies
+            L._s.committed, L._s.n_live = s.committed, s.n_live

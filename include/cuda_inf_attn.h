@@ -51,6 +51,7 @@ extern "C" {
 #define CIA_HEAD_DIM 64      /* (engine.cu:35) */
 #define CIA_KVGROUP 64       /* tokens per FP8 group   (engine.cu:23) */
 #define CIA_E4M3_MAX 448.0f  /* (engine.cu:22) */
+#define CIA_HIDDEN 2048       /* hidden size H          (engine.cu:33) */
 #define CIA_NSPLIT_DEFAULT 16   /* the reference's NSPLIT (engine.cu:392) */
 #define CIA_NSPLIT_MAX 4096
 
@@ -373,6 +374,42 @@ int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
                     const uint16_t* k, const uint16_t* v, uint16_t* out,
                     int past, int steps, float scale, void** events,
                     void* stream);
+
+/* INT4 projection weights of one attention layer (the Q4 tensors
+ * self_attn.{q,k,v,out}_proj.weight of engine.cu:792-797, 858) and the
+ * scratch their outputs live in. */
+typedef struct cia_attn_proj {
+  const uint8_t* q_packed; const uint16_t* q_scales; /* [2048][1024], [2048][16] */
+  const uint8_t* k_packed; const uint16_t* k_scales; /* [512][1024],  [512][16]  */
+  const uint8_t* v_packed; const uint16_t* v_scales; /* [512][1024],  [512][16]  */
+  const uint8_t* o_packed; const uint16_t* o_scales; /* [2048][1024], [2048][16] */
+  uint16_t* ws; /* device fp16 scratch of cap * 5120 elements: q, k, v and the
+                   attention output of up to cap tokens */
+  int cap;
+} cia_attn_proj;
+
+/* The attention branch of one layer (engine.cu:792-859): x fp16 [S][2048]
+ * (operator_norm's output) -> q, k, v in one launch (cia_qkv_proj_int4),
+ * the QK producers (when L->qw is set) and attention through
+ * cia_layer_forward, then out_proj added into the residual h fp32
+ * [S][2048] in one launch (cia_gemv_int4_add).  S <= P->cap.  A
+ * single-token step on a group-64 layer with L->qw set is four launches
+ * (projections, attend, finish, out_proj) where the reference makes
+ * fourteen. */
+int cia_attn_block_forward(cia_layer* L, const cia_attn_proj* P,
+                           const uint16_t* x, float* h, int S, int past,
+                           float scale, int* evicted, void* stream);
+
+/* Decode steps of the attention branches: for step s and layer l runs
+ * cia_attn_block_forward(&layers[l], &proj[l], x[s][l], h, 1, past + s).
+ * x: fp16 [steps][n_layers][2048]; h: fp32 [2048], the residual stream
+ * every layer adds into.  events (may be NULL): 4*steps*n_layers
+ * hipEvent_t; for r = s*n_layers + l, events[4r] precedes the projections,
+ * events[4r+1] follows them, events[4r+2] follows the attention and
+ * events[4r+3] the out_proj. */
+int cia_attn_block_loop(cia_layer* layers, const cia_attn_proj* proj,
+                        int n_layers, const uint16_t* x, float* h, int past,
+                        int steps, float scale, void** events, void* stream);
 
 #ifdef __cplusplus
 }

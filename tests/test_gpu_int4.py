@@ -55,6 +55,9 @@ CASES = [
     (2048, 4096, 2, "normal", 5),
     (64, 2048, 1, "extreme", 6),
     (512, 2048, 9, "normal", 7),
+    (2048, 2048, 96, "normal", 8),   # matrix-core path from 80 rows of x
+    (100, 384, 200, "normal", 9),    # ragged tiles in both directions
+    (520, 2048, 300, "extreme", 13),
 ]
 
 
@@ -79,7 +82,7 @@ def test_gemv_int4(orc, cia, dev, N, K, M, kind, seed):
            extra=2 * np.finfo(np.float32).eps * (np.abs(y0) + np.abs(ref)))
 
 
-@pytest.mark.parametrize("M,seed", [(1, 10), (3, 11), (6, 12)])
+@pytest.mark.parametrize("M,seed", [(1, 10), (3, 11), (6, 12), (130, 14)])
 def test_qkv_proj_int4(orc, cia, dev, M, seed):
     """q/k/v in one launch with the fp16 conversion fused: each output is
     the fp16 rounding of the same kernel's fp32 sum (compared with the fp32
