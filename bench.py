@@ -373,6 +373,49 @@ def main():
         log(f"prefill {S}: attention {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s; "
             f"append + attention {lms * 1e3:.1f} us; fp8 {f8ms * 1e3:.1f} us "
             f"({prefill['fp8']['tflops']} TFLOP/s), max |fp8 - fp16| {float(d8.max()):.4f}")
+        # the layer's INT4 projections over the S prompt rows (matrix-core
+        # GEMM): q/k/v in one launch, out_proj into the residual
+        H = _lib.HIDDEN
+        gp = torch.Generator(device=dev)
+        gp.manual_seed(29)
+        wts = {}
+        for name, N in (("q", NH * D), ("k", NKV * D), ("v", NKV * D), ("o", H)):
+            wts[name] = (torch.randint(0, 256, (N, H // 2), generator=gp, device=dev,
+                                       dtype=torch.uint8),
+                         (0.002 + 0.018 * torch.rand((N, H // 128), generator=gp,
+                                                     device=dev)).half())
+        xp = torch.randn((S, H), generator=gp, device=dev).half()
+        hp = torch.zeros((S, H), dtype=torch.float32, device=dev)
+        pq = torch.empty((S, NH * D), dtype=torch.float16, device=dev)
+        pk = torch.empty((S, NKV * D), dtype=torch.float16, device=dev)
+        pv = torch.empty_like(pk)
+        Kn.qkv_proj_int4(xp, wts["q"], wts["k"], wts["v"], pq, pk, pv, S, H)
+        Kn.gemv_int4(pq, *wts["o"], hp, H, NH * D, S, add=True)
+        torch.cuda.synchronize()
+        p0.record(stream)
+        for _ in range(reps):
+            Kn.qkv_proj_int4(xp, wts["q"], wts["k"], wts["v"], pq, pk, pv, S, H)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        qkv_ms = p0.elapsed_time(p1) / reps
+        p0.record(stream)
+        for _ in range(reps):
+            Kn.gemv_int4(pq, *wts["o"], hp, H, NH * D, S, add=True)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        o_ms = p0.elapsed_time(p1) / reps
+        f_qkv = 2.0 * S * H * (NH * D + 2 * NKV * D)
+        f_o = 2.0 * S * H * NH * D
+        prefill["int4_projections"] = {
+            "kernel": "k_gemm_int4 (v_mfma_f32_16x16x32_f16, exact nibble operands, "
+                      "per-group fp32 scaling)",
+            "qkv_us": round(qkv_ms * 1e3, 1),
+            "qkv_tflops": round(f_qkv / (qkv_ms * 1e-3) / 1e12, 1),
+            "out_proj_residual_us": round(o_ms * 1e3, 1),
+            "out_proj_tflops": round(f_o / (o_ms * 1e-3) / 1e12, 1),
+            "mfma_f16_frac": round((f_qkv + f_o) / ((qkv_ms + o_ms) * 1e-3) / 1e12
+                                   / MFMA_F16_PEAK_TFLOPS, 4)}
+        log(f"prefill {S}: INT4 q/k/v {qkv_ms * 1e3:.1f} us, out_proj {o_ms * 1e3:.1f} us")
 
     cpu_layer, cpu_committed = layers[0], arr[0].committed
 
