@@ -382,11 +382,12 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
       kq[cc] = *(const u32x4*)(kp + 8 * cc);
       qq[cc] = *(const u32x4*)(qp + 8 * cc);
     }
+    // (this lane's 8 V dims on their own: indexing the full row below with
+    // the runtime c would put it in scratch memory)
+    vv = *(const u32x4*)(vp + 8 * c);
     if (commit) {
 #pragma unroll
       for (int cc = 0; cc < 8; cc++) vrow[cc] = *(const u32x4*)(vp + 8 * cc);
-    } else {
-      vv = *(const u32x4*)(vp + 8 * c);
     }
   }
   // the fresh token joins the tail, written once per kv head
@@ -459,8 +460,9 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     x = sacc * (a.scale * kLog2e);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const uint32_t vb = e4m3x4(vfl[8 * c + 4 * j] / scv, vfl[8 * c + 4 * j + 1] / scv,
-                                 vfl[8 * c + 4 * j + 2] / scv, vfl[8 * c + 4 * j + 3] / scv);
+      const uint32_t vb = e4m3x4(h2f((uint16_t)vv[2 * j]) / scv, h2f((uint16_t)(vv[2 * j] >> 16)) / scv,
+                                 h2f((uint16_t)vv[2 * j + 1]) / scv,
+                                 h2f((uint16_t)(vv[2 * j + 1] >> 16)) / scv);
       vf[4 * j] = e4m3_to_f32<0>(vb) * vdq;
       vf[4 * j + 1] = e4m3_to_f32<1>(vb) * vdq;
       vf[4 * j + 2] = e4m3_to_f32<2>(vb) * vdq;
