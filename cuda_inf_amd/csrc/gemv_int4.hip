@@ -41,7 +41,7 @@ struct GemvArgs {
 };
 
 constexpr int kGemvWaves = 8;
-constexpr int kGemmMinM = 80;  // rows of x from which the matrix-core GEMM runs (measured crossover)
+constexpr int kGemmMinM = 56;  // rows of x from which the matrix-core GEMM runs (measured crossover)
 
 // nibbles sh..sh+3 and sh+16..sh+19 of w as fp16 (nibble - 8), exact
 __device__ __forceinline__ f16x2 nib_pair(uint32_t w, int sh) {
@@ -186,21 +186,37 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv_int4(GemvArgs a) {
 // ---------------------------------------------------------------- GEMM
 // Many rows of x (prefill): Y = X W^T on the fp16 matrix cores
 // (v_mfma_f32_16x16x32_f16).  A workgroup computes a 128 (x rows) x 128
-// (weight rows) tile with 4 waves in a 2 x 2 grid of 64 x 64 wave tiles
-// (4 x 4 MFMA tiles).  The K loop runs over the 128-wide scale groups: the
+// (weight rows) tile with 8 waves (two per SIMD, so one wave's matrix
+// products overlap another's dequantisation) in a 2 x 4 grid of 64 x 32
+// wave tiles (4 x 2 MFMA tiles).  The K loop runs over the 128-wide scale groups: the
 // products of one group accumulate from zero on the matrix cores and are
 // then added with the group scale of their column in fp32, so the weights
 // enter the MFMA as exact fp16 (nibble - 8) values.
 //   Inside a group the k order of the four 32-k MFMA steps is permuted the
 //   same way for both operands: lane group q = l >> 4 holds k = 32q + 8s ..
-//   32q + 8s + 7 at step s.  So one 16-byte load per lane and column tile
-//   brings the nibbles of all four steps (k = 32q .. 32q+31), word s being
-//   step s.
-//   X tiles go through LDS (two buffers, 32 KiB each): row r, 16-byte chunk
-//   c at chunk c ^ (r & 15), so the 16 rows of an MFMA read hit distinct
-//   banks.  The next group's X and weights are loaded while this group
-//   computes; one barrier per group.
+//   32q + 8s + 7 at step s, so one 16-byte read per lane and column tile
+//   brings the nibbles of all four steps (word s is step s).
+//   Operands reach LDS by DMA (global_load_lds_dwordx4: lane i's 16 bytes
+//   land at the instruction's LDS base + 16 i, so the swizzles are made by
+//   choosing which global chunk each lane fetches), in a ring of 3 slots
+//   filled two groups ahead: per group one wait for the group's own DMA,
+//   one barrier, and no staging registers.
+//     X slot: 128 rows x 16 chunks; row r's chunk c at c ^ (r & 15) (the 16
+//       rows of an MFMA read hit distinct banks).
+//     W slot: 128 columns x 4 chunks of nibbles; column c's chunk q at
+//       q ^ ((c >> 2) & 3) (16 consecutive columns hit distinct banks).
+//     scale slot: the 128 columns' fp16 scales of the group, one per dword
+//       (a 2-byte LDS DMA writes each lane's value zero-extended to a dword).
 constexpr int kTile = 128;
+constexpr int kRing = 3;
+constexpr int kGemmWaves = 8;
+constexpr int kXSlot = kTile * 256;            // bytes: 128 rows x 128 fp16
+constexpr int kWSlot = kTile * 64;             // bytes: 128 columns x 128 nibbles
+constexpr int kSSlot = 2 * kTile * 4;          // bytes: 128 scale dwords + a drop area
+constexpr int kSlot = kXSlot + kWSlot + kSSlot;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
 
 // 8 nibbles (one u32, k even in the low nibble) -> 8 fp16 (nibble - 8), in k order
 __device__ __forceinline__ f16x8 nib8(uint32_t u) {
@@ -219,110 +235,119 @@ __device__ __forceinline__ f16x8 nib8(uint32_t u) {
   return r;
 }
 
-// grid = (ceil(rows / 128), ceil(M / 128)), block = 256
-__global__ __launch_bounds__(256) void k_gemm_int4(GemvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kTile * 128];
+// weight row of global column col (clamped), across the up to 3 matrices
+struct ColRef {
+  const uint8_t* packed;
+  const uint16_t* scales;
+};
+__device__ __forceinline__ ColRef col_ref(const GemvArgs& a, int col, int K) {
+  int n = col < a.rows ? col : a.rows - 1, mi = 0;
+  if (n >= a.mat[0].N) {
+    n -= a.mat[0].N;
+    mi = 1;
+    if (n >= a.mat[1].N) {
+      n -= a.mat[1].N;
+      mi = 2;
+    }
+  }
+  const uint8_t* pk = mi == 0 ? a.mat[0].packed : (mi == 1 ? a.mat[1].packed : a.mat[2].packed);
+  const uint16_t* sc = mi == 0 ? a.mat[0].scales : (mi == 1 ? a.mat[1].scales : a.mat[2].scales);
+  return ColRef{pk + (size_t)n * (K >> 1), sc + (size_t)n * (K >> 7)};
+}
+
+// grid = (ceil(rows / 128), ceil(M / 128)), block = 64 * kGemmWaves.
+// (Giving each XCD a contiguous run of tiles, so its L2 sees a few row
+// blocks of X rather than all, measured no faster.)
+__global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kRing * kSlot];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int wm = w >> 1, wn = w & 1, n16 = l & 15, q = l >> 4;
+  const int wm = w >> 2, wn = w & 3, n16 = l & 15, q = l >> 4;
   const int m0 = blockIdx.y * kTile, r0 = blockIdx.x * kTile;
   const int K = a.K, ng = K >> 7;
-  // this lane's weight row in each of the wave's 4 column tiles
-  const uint8_t* wrow[4];
-  const uint16_t* srow[4];
+  // DMA sources of this lane (fixed across groups; + 256 g bytes for X,
+  // + 64 g for W, + 2 g for the scales)
+  //   X: instruction t of wave w fills rows 4 (4w + t) .. +3; lane l takes
+  //      row 4 (4w + t) + (l >> 4), physical chunk l & 15
+  const uint8_t* xsrc[4];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    int n = r0 + 64 * wn + 16 * j + n16;
-    n = n < a.rows ? n : a.rows - 1;
-    int mi = 0;
-    if (n >= a.mat[0].N) {
-      n -= a.mat[0].N;
-      mi = 1;
-      if (n >= a.mat[1].N) {
-        n -= a.mat[1].N;
-        mi = 2;
-      }
-    }
-    const uint8_t* pk = mi == 0 ? a.mat[0].packed : (mi == 1 ? a.mat[1].packed : a.mat[2].packed);
-    const uint16_t* sc = mi == 0 ? a.mat[0].scales : (mi == 1 ? a.mat[1].scales : a.mat[2].scales);
-    wrow[j] = pk + (size_t)n * (K >> 1) + 16 * q;
-    srow[j] = sc + (size_t)n * ng;
+  for (int t = 0; t < 4; t++) {
+    const int r = 4 * (4 * w + t) + (l >> 4), m = m0 + r;
+    const int lc = (l & 15) ^ (r & 15);
+    xsrc[t] = (const uint8_t*)(a.x + (size_t)(m < a.M ? m : a.M - 1) * K) + 16 * lc;
   }
-  // X staging: pass p moves rows 16p + (tid >> 4), chunk tid & 15
-  const int sr = tid >> 4, sc16 = tid & 15;
-  const uint16_t* xrow[8];
+  //   W: wave w fills columns 16 w .. +15; lane l takes column 16 w + (l >> 2),
+  //      physical chunk l & 3
+  const int wcol = 16 * w + (l >> 2);
+  const uint8_t* wsrc = col_ref(a, r0 + wcol, K).packed + 16 * ((l & 3) ^ ((wcol >> 2) & 3));
+  //   scales: waves 0, 1 fill columns 64 w + l; the others the drop area
+  const uint16_t* ssrc = col_ref(a, r0 + 64 * (w & 1) + l, K).scales;
+  const int sdst = kXSlot + kWSlot + (w < 2 ? 256 * w : 512);
+  auto issue = [&](int g) {
+    uint8_t* slot = ring + (g % kRing) * kSlot;
+    const int gg = g < ng ? g : ng - 1;  // past the end: a harmless refetch
 #pragma unroll
-  for (int p = 0; p < 8; p++) {
-    const int m = m0 + 16 * p + sr;
-    xrow[p] = a.x + (size_t)(m < a.M ? m : a.M - 1) * K + 8 * sc16;
-  }
-  const int xdst = sr * 128 + 8 * (sc16 ^ (sr & 15));  // + 16 * 128 * p
-  u32x4 xv[8], wv[4];
-  uint32_t sv[4];
-  auto load = [&](int g) {
-#pragma unroll
-    for (int p = 0; p < 8; p++) xv[p] = *(const u32x4*)(xrow[p] + 128 * g);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      wv[j] = *(const u32x4*)(wrow[j] + 64 * g);
-      sv[j] = srow[j][g];
-    }
+    for (int t = 0; t < 4; t++)
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(xsrc[t] + 256 * gg),
+                                       (lds_void_t*)(slot + (4 * w + t) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)(wsrc + 64 * gg),
+                                     (lds_void_t*)(slot + kXSlot + w * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)(ssrc + gg), (lds_void_t*)(slot + sdst), 2, 0,
+                                     0);
   };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < 8; p++) *(u32x4*)(&xs[buf][16 * 128 * p + xdst]) = xv[p];
-  };
-  f32x4 C[4][4];
+  f32x4 C[4][2];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) C[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  load(0);
-  stage(0);
-  __syncthreads();
+    for (int j = 0; j < 2; j++) C[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  issue(0);
+  issue(1);
   for (int g = 0; g < ng; g++) {
-    const int buf = g & 1;
-    u32x4 wc[4];
-    float scl[4];
+    // this group's 6 DMAs are done once at most the next group's 6 remain
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    __builtin_amdgcn_s_barrier();        // every wave's DMA landed; slot g-1 is free
+    issue(g + 2);
+    const uint8_t* slot = ring + (g % kRing) * kSlot;
+    const uint16_t* xs = (const uint16_t*)slot;
+    const uint8_t* ws = slot + kXSlot;
+    const uint32_t* ss = (const uint32_t*)(slot + kXSlot + kWSlot);
+    u32x4 wq[2];
+    float scl[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      wc[j] = wv[j];
-      scl[j] = h2f((uint16_t)sv[j]);
+    for (int j = 0; j < 2; j++) {
+      const int c = 32 * wn + 16 * j + n16;
+      wq[j] = *(const u32x4*)(ws + c * 64 + 16 * (q ^ ((c >> 2) & 3)));
+      scl[j] = h2f((uint16_t)ss[c]);
     }
-    if (g + 1 < ng) load(g + 1);
-    f32x4 P[4][4];
+    f32x4 P[4][2];
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      f16x8 A[4], B[4];
+    for (int s2 = 0; s2 < 4; s2++) {
+      f16x8 A[4], B[2];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int r = 64 * wm + 16 * i + n16;
-        A[i] = *(const f16x8*)(&xs[buf][r * 128 + 8 * ((4 * q + s) ^ n16)]);
+        A[i] = *(const f16x8*)(xs + r * 128 + 8 * ((4 * q + s2) ^ n16));
       }
 #pragma unroll
-      for (int j = 0; j < 4; j++) B[j] = nib8(wc[j][s]);
+      for (int j = 0; j < 2; j++) B[j] = nib8(wq[j][s2]);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
           P[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              A[i], B[j], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[i][j], 0, 0, 0);
+              A[i], B[j], s2 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : P[i][j], 0, 0, 0);
     }
     // C += P * scale of the column (the lane's column is n16 of tile j)
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int e = 0; e < 4; e++) C[i][j][e] = __builtin_fmaf(P[i][j][e], scl[j], C[i][j][e]);
-    if (g + 1 < ng) {
-      stage(buf ^ 1);
-      __syncthreads();
-    }
   }
   // outputs: lane holds rows 4q + e of tile i, column n16 of tile j
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int col = r0 + 64 * wn + 16 * j + n16;
+  for (int j = 0; j < 2; j++) {
+    const int col = r0 + 32 * wn + 16 * j + n16;
     if (col >= a.rows) continue;
     int n = col, mi = 0;
     if (n >= a.mat[0].N) {
@@ -348,6 +373,9 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemvArgs a) {
         if (y16) y16[o] = f2h(v);
       }
   }
+  // (the last two DMAs refetch the final group into free slots; let them
+  // land before the workgroup's LDS is released)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 }
 
 template <int kM>
@@ -371,7 +399,7 @@ static int gemv_run(GemvArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a.M >= kGemmMinM) {
     hipLaunchKernelGGL(k_gemm_int4, dim3((unsigned)((a.rows + kTile - 1) / kTile),
-                       (unsigned)((a.M + kTile - 1) / kTile)), dim3(256), 0, s, a);
+                       (unsigned)((a.M + kTile - 1) / kTile)), dim3(64 * kGemmWaves), 0, s, a);
   } else if (a.M == 1)
     gemv_launch<1>(a, s);
   else if (a.M == 2)

@@ -55,7 +55,7 @@ CASES = [
     (2048, 4096, 2, "normal", 5),
     (64, 2048, 1, "extreme", 6),
     (512, 2048, 9, "normal", 7),
-    (2048, 2048, 96, "normal", 8),   # matrix-core path from 80 rows of x
+    (2048, 2048, 96, "normal", 8),   # matrix-core path from 56 rows of x
     (100, 384, 200, "normal", 9),    # ragged tiles in both directions
     (520, 2048, 300, "extreme", 13),
 ]
