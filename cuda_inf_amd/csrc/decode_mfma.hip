@@ -53,13 +53,20 @@ __device__ __forceinline__ f16x8 cvt8(uint32_t w0, uint32_t w1) {
   return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-// LDS tile offsets: 32 keys x 256 bytes, chunk c (16 B, 0..15) of key k.
-// K: the 16 keys of a tile read the same logical chunk -> XOR with key & 15.
-// V: the 8 keys {4b..4b+3, 16+4b..16+4b+3} of one transposed read
-//    share a logical chunk -> XOR with a 3-bit function distinct on them.
-__device__ __forceinline__ int kaddr(int key, int c) { return key * 256 + ((c ^ (key & 15)) << 4); }
-__device__ __forceinline__ int vswz(int key) { return (key & 3) | (((key >> 4) & 1) << 2); }
-__device__ __forceinline__ int vaddr(int key, int c) { return key * 256 + ((c ^ vswz(key)) << 4); }
+// LDS tiles of a pair: 32 keys x 256 bytes, rows padded to 272 bytes and
+// keys 16..31 shifted by a further 64 bytes.  Row r starts 16 r bytes into a
+// 128-byte bank cycle, so each 8-lane group of a 16-byte access (K/V stores:
+// one key row; K operand reads: 8 keys, one chunk) and each 16-lane group of
+// the transposed V reads (keys 4b..4b+3 and 16+4b..16+4b+3, the second four
+// moved to the other half of the cycle by the shift) touches distinct banks,
+// and every address is a per-lane base plus an immediate.
+constexpr int kRowB = 272;
+constexpr int kTileB = 16 * kRowB + 64;  // byte offset of keys 16..31
+constexpr int kPairB = 2 * kTileB;       // 8832 bytes per wave and operand
+constexpr int kQRowsB = 16 * D * 2;      // q rows of a half (fp16)
+constexpr int kQBytes = kQRowsB + 128;   // + 128 zero bytes (inactive operand lanes)
+constexpr int kMRow = D + 4;             // merge rows (floats)
+__device__ __forceinline__ int lds_row(int key) { return key * kRowB + (key >> 4) * 64; }
 
 struct DecodeArgs {
   const uint16_t* q;  // [32][64]
@@ -86,80 +93,99 @@ struct DecodeArgs {
 // kPrep: q arrives raw and the QK producers run here (a.prep)
 template <bool kPrep>
 __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t klds[kDecWaves][32 * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t vlds[kDecWaves][32 * 256];
-  __shared__ float sm[kDecWaves][16], sl[kDecWaves][16];
-  __shared__ __attribute__((aligned(16))) uint16_t qprep[16 * D];
+  __shared__ __attribute__((aligned(16))) uint8_t klds[kDecWaves][kPairB];
+  __shared__ __attribute__((aligned(16))) uint8_t vlds[kDecWaves][kPairB];
+  // q rows of the half (fp16) + zeros: the wave's own copy (prepared q), or
+  // one copy the producers fill (raw q)
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[kPrep ? 1 : kDecWaves][kQBytes];
   const int half = blockIdx.y;
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, l = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = l & 15, b = l >> 4;  // MFMA column / k-group of this lane
   uint8_t* kw = klds[w];
   uint8_t* vw = vlds[w];
+  uint8_t* qb = qlds[kPrep ? 0 : w];
   // this wave's pairs: an even share of the half's pairs
   const int nwaves = a.nwg * kDecWaves;
   const int wid = blockIdx.x * kDecWaves + w;
   // (wid * npairs < 2^31: at most 1024 waves per half, 2^21 pairs)
   const int p0 = (int)(((unsigned)wid * (unsigned)a.npairs) / (unsigned)nwaves);
   const int p1 = (int)(((unsigned)(wid + 1) * (unsigned)a.npairs) / (unsigned)nwaves);
-  // Q^T as the block-diagonal B operand, fp16.  Prepared q is loaded before
-  // the first pair; raw q (with the QK producers) is loaded first too, but
-  // normalised and rotated while the first pair's K/V loads are in flight.
-  f16x8 qop[8];
-  // (32-bit holders: packing two loaded halves into one register would
-  // wait for both loads on the spot)
+  // Q^T as the block-diagonal B operand, fp16, read from LDS: lane (n, b)
+  // holds query head n of the half when its k-group b is that head's kv head
+  // (n >> 2), zeros otherwise.  Prepared q: the half's 2 KiB arrive in two
+  // full-wave loads issued before the first pair (eight 16-lane operand loads
+  // per wave measurably slow the K/V stream behind them).  Raw q (with the
+  // QK producers) is loaded first too, but normalised and rotated while the
+  // first pair's K/V loads are in flight.
   uint32_t qraw[2] = {0u, 0u}, wraw = 0u;
+  u32x4 qrow2[2];
   float invf = 0.0f;
   if constexpr (kPrep) {
     invf = a.prep.rt.invf[l & 31];
     wraw = a.prep.qw[l];
 #pragma unroll
     for (int r = 0; r < 2; r++) qraw[r] = a.q[(size_t)(half * 16 + 2 * w + r) * D + l];
-  } else if ((n >> 2) == b) {
-    const uint16_t* qp = a.q + (size_t)(half * 16 + n) * D;
-#pragma unroll
-    for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qp + 8 * mu);
   } else {
 #pragma unroll
-    for (int mu = 0; mu < 8; mu++) qop[mu] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int r = 0; r < 2; r++)
+      qrow2[r] = *(const u32x4*)(a.q + (size_t)half * 16 * D + (size_t)(r * 64 + l) * 8);
   }
+  // per-lane address parts (bytes): global rows of a pair, K/V stores,
+  // K operand reads, V transposed reads
+  const uint32_t goff = (uint32_t)(b * 512 + n * 16);
+  const int wr = b * kRowB + n * 16;  // store i -> key 4i + b, chunk n
+  const int krd = n * kRowB + b * 64;  // tile t, MFMA pair m2 -> key 16t + n, chunk 4b + m2
+  const int kk8 = n >> 1;
+  const int vkey = kk8 < 4 ? 4 * b + kk8 : 16 + 4 * b + (kk8 - 4);
+  int vrd[4];  // MFMA mu reads kv head (b + mu) & 3; + nu * 16
+#pragma unroll
+  for (int mu = 0; mu < 4; mu++) vrd[mu] = lds_row(vkey) + 8 * (n & 1) + ((b + mu) & 3) * 64;
   // loads of a pair: instruction i covers keys 4i..4i+3, lane -> (key 4i + b,
-  // chunk n); the group scales first, then all K, then all V, so S^T and the
-  // softmax run while V is still arriving
+  // chunk n); the group scales first (both for this lane's column kv head),
+  // then all K, then all V, so S^T and the softmax run while V is still
+  // arriving
   uint16_t ksc_h = 0, vsc_h = 0;
   u32x4 kr[8], vr[8];
-  auto load_pair = [&](int p, const uint8_t* kc8, const uint8_t* vc8) {
-    const int kbase = p * 32, grp = kbase >> 6;
-    ksc_h = a.ksc[grp * NKV + half * 4 + (n >> 2)];
-    vsc_h = a.vsc[grp * NKV + half * 4 + b];
+  auto load_k = [&](int p, const uint8_t* kc8) {
+    const uint8_t* kb = kc8 + (size_t)p * (32 * 512) + half * 256;
+    ksc_h = a.ksc[(p >> 1) * NKV + half * 4 + (n >> 2)];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      kr[i] = *(const u32x4*)(kc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+    for (int i = 0; i < 8; i++) kr[i] = *(const u32x4*)(kb + goff + i * 2048);
+  };
+  auto load_v = [&](int p, const uint8_t* vc8) {
+    const uint8_t* vb = vc8 + (size_t)p * (32 * 512) + half * 256;
+    vsc_h = a.vsc[(p >> 1) * NKV + half * 4 + (n >> 2)];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      vr[i] = *(const u32x4*)(vc8 + (size_t)(kbase + 4 * i + b) * 512 + half * 256 + n * 16);
+    for (int i = 0; i < 8; i++) vr[i] = *(const u32x4*)(vb + goff + i * 2048);
   };
   // The first pair is loaded whether or not the wave has one (a wave
   // without pairs reads pair 0, or with no committed pair at all the first
   // 16 KiB of the tail buffers, and never uses the values).  It is issued
-  // in two phases per workgroup: waves 0-3, a barrier, then waves 4-7 (which
-  // in the compiled code also wait for their own q loads first).  With
+  // in two phases per workgroup: waves 0-3, a barrier, then waves 4-7.  With
   // every wave's loads issued at once, each wave's last bytes land at the
   // end of the launch and all arithmetic queues behind them; staggered,
-  // the first half computes while the second half streams in (measured:
-  // 2.5-3.4 % less time per decode token at 32k).  With the QK producers
-  // the workgroup meets at a barrier anyway, and a stagger there costs 2 %:
-  // all waves issue at once.
+  // the first half computes while the second half streams in.  With the QK
+  // producers the workgroup meets at a barrier anyway, and all waves issue
+  // at once.
   {
     const bool cache = p0 < p1 || a.npairs > 0;
     const int pf = p0 < p1 ? p0 : 0;
     const uint8_t* k8 = cache ? a.kc8 : (const uint8_t*)a.ktail;
     const uint8_t* v8 = cache ? a.vc8 : (const uint8_t*)a.vtail;
     if constexpr (kPrep) {
-      load_pair(pf, k8, v8);
+      load_k(pf, k8);
+      load_v(pf, v8);
     } else {
-      if (w < kDecWaves / 2) load_pair(pf, k8, v8);
-      __builtin_amdgcn_s_barrier();
-      if (w >= kDecWaves / 2) load_pair(pf, k8, v8);
+      // One load in straight-line code, the barrier on either side of it by
+      // wave (each wave executes one barrier; the hardware counts arrivals).
+      // Loads under two conditional branches would merge at the joins into a
+      // conservative count, and every later wait on a pair register would
+      // become a wait for all of the wave's loads.
+      if (w >= kDecWaves / 2) __builtin_amdgcn_s_barrier();
+      load_k(pf, k8);
+      load_v(pf, v8);
+      if (w < kDecWaves / 2) __builtin_amdgcn_s_barrier();
     }
   }
   if constexpr (kPrep) {
@@ -167,37 +193,46 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
     // waits only for its own older loads)
     __builtin_amdgcn_sched_barrier(0);
     // the QK producers on the half's 16 query heads: two per wave, one dim
-    // per lane, into LDS
+    // per lane, into LDS; wave 0 also writes the zero bytes
     float sn, cs;
     rope_sincos_f(invf, a.qpos, sn, cs);
     const float wq = h2f((uint16_t)wraw);
+    uint16_t* qrows = (uint16_t*)qb;
 #pragma unroll
     for (int r = 0; r < 2; r++)
-      qprep[(2 * w + r) * D + l] =
+      qrows[(2 * w + r) * D + l] =
           qk_norm_rope_sc(h2f((uint16_t)qraw[r]), wq, l, sn, cs, a.prep.eps);
+    if (w == 0 && l < 8) *(u32x4*)(qb + kQRowsB + 16 * l) = u32x4{0u, 0u, 0u, 0u};
     // LDS writes done, then the barrier alone: a full __syncthreads would
     // also wait for the first pair's K/V loads
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    if ((n >> 2) == b) {
+  } else {
+    // (one wave writes and reads its own copy: LDS executes a wave's
+    // instructions in order, the wave barrier keeps the compiler from
+    // reordering them)
 #pragma unroll
-      for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qprep + n * D + 8 * mu);
-    } else {
+    for (int r = 0; r < 2; r++) *(u32x4*)(qb + (r * 64 + l) * 16) = qrow2[r];
+    if (l < 8) *(u32x4*)(qb + kQRowsB + 16 * l) = u32x4{0u, 0u, 0u, 0u};
+    __builtin_amdgcn_wave_barrier();
+  }
+  f16x8 qop[8];
+  {
+    const int qoff = (n >> 2) == b ? n * (2 * D) : kQRowsB;
 #pragma unroll
-      for (int mu = 0; mu < 8; mu++) qop[mu] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int mu = 0; mu < 8; mu++) qop[mu] = *(const f16x8*)(qb + qoff + 16 * mu);
   }
   const float qscale = a.scale * kLog2e;
+  const f16x2 one2 = f16x2{(_Float16)1.0f, (_Float16)1.0f};
   float mx = -1e30f, lsum = 0.f;  // column (a, j) = n: running max (log2) and sum
   f32x4 O[4];                     // rows (kv head b, query head i), dims 16 nu + n
 #pragma unroll
   for (int v = 0; v < 4; v++) O[v] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p = p0; p < p1; p++) {
-    if (p != p0) load_pair(p, a.kc8, a.vc8);
-    // K scale of this lane's column kv head (times scale*log2e), V scale of
-    // this lane's row kv head
+    // K scale of this lane's column kv head (times scale*log2e); V scale of
+    // the same kv head, folded into P
     const float ksc = h2f(ksc_h) * qscale;
-    const float vsc = h2f(vsc_h);
+    const _Float16 vsc = __builtin_bit_cast(_Float16, vsc_h);
     // ---- S^T = K Q^T for the pair's two tiles; tile t (keys 16t..16t+15)
     // needs only load instructions 4t..4t+3
     f32x4 S[2];
@@ -207,15 +242,19 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
       // for their loads, behind this tile's matrix products)
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 4 * t; i < 4 * t + 4; i++) *(u32x4*)(kw + kaddr(4 * i + b, n)) = kr[i];
+      for (int i = 4 * t; i < 4 * t + 4; i++)
+        *(u32x4*)(kw + wr + (i & 3) * (4 * kRowB) + (i >> 2) * kTileB) = kr[i];
       S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m2 = 0; m2 < 4; m2++) {
-        const u32x4 kk = *(const u32x4*)(kw + kaddr(16 * t + n, b * 4 + m2));
+        const u32x4 kk = *(const u32x4*)(kw + krd + t * kTileB + 16 * m2);
         S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[0], kk[1]), qop[2 * m2], S[t], 0, 0, 0);
         S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[2], kk[3]), qop[2 * m2 + 1], S[t], 0, 0, 0);
       }
     }
+    // the next pair's K loads go out as soon as this pair's K is in LDS
+    const bool more = p + 1 < p1;
+    if (more) load_k(p + 1, a.kc8);
     // ---- online softmax (column (a, j) = n: 4 lanes x 4 keys per tile)
     float rmx = -1e30f;
 #pragma unroll
@@ -230,29 +269,28 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
     const float corr = __builtin_amdgcn_exp2f(mx - mnew);  // rescales earlier rounds
     mx = mnew;
     f16x8 P;
-    float rs = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const _Float16 ph = (_Float16)__builtin_amdgcn_exp2f(S[t][i] - mnew);
-        P[t * 4 + i] = ph;
-        rs += (float)ph;
-      }
+      for (int i = 0; i < 4; i++) P[t * 4 + i] = (_Float16)__builtin_amdgcn_exp2f(S[t][i] - mnew);
+    // row sum of the fp16 numerators (the weights P V uses, before the V scale)
+    float rs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) rs = __builtin_amdgcn_fdot2(f16x2{P[2 * e], P[2 * e + 1]}, one2, rs, false);
     rs = col4_sum(rs);
     lsum = __builtin_fmaf(lsum, corr, rs);
+    P = P * vsc;
     // this lane's O rows are (kv head b, query head i); the correction of
     // column (b, i) lives in lane 4b + i
     float oc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) oc[i] = __shfl(corr, 4 * b + i);
-    // ---- O = O * corr + sv * (P V)
+    // ---- O = O * corr + (P sv) V
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) *(u32x4*)(vw + vaddr(4 * i + b, n)) = vr[i];
+    for (int i = 0; i < 8; i++)
+      *(u32x4*)(vw + wr + (i & 3) * (4 * kRowB) + (i >> 2) * kTileB) = vr[i];
     const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    const int kk8 = n >> 1, hb = n & 1;
-    const int key = kk8 < 4 ? 4 * b + kk8 : 16 + 4 * b + (kk8 - 4);
     f32x4 T[4];
 #pragma unroll
     for (int nu = 0; nu < 4; nu++) T[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -263,47 +301,48 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
 #pragma unroll
       for (int nu = 0; nu < 4; nu++) {
         const u32x2 raw = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                       (lds_i32x2*)(vw + vaddr(key, sg * 4 + nu) + 8 * hb)));
+            u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(vw + vrd[mu] + 16 * nu)));
         T[nu] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw[0], raw[1]), T[nu], 0, 0, 0);
       }
     }
+    if (more) load_v(p + 1, a.vc8);
 #pragma unroll
     for (int nu = 0; nu < 4; nu++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) O[nu][i] = __builtin_fmaf(vsc, T[nu][i], O[nu][i] * oc[i]);
+      for (int i = 0; i < 4; i++) O[nu][i] = __builtin_fmaf(O[nu][i], oc[i], T[nu][i]);
   }
-  // ---- merge the waves (rows r = 4a + j); the K tiles hold the O rows now
+  // ---- merge the waves: O per wave in the V tiles, rows of 68 floats (the
+  // readers' 8-byte loads of one row are contiguous; the stores of a fixed
+  // (nu, i) conflict at most 2 ways); (m, l) per row in the K tiles
   __syncthreads();
-  typedef float MergeRows[16][D + 1];
-  MergeRows* sO = (MergeRows*)&klds[0][0];
-  if (l < 16) {
-    sm[w][l] = mx;
-    sl[w][l] = lsum;
-  }
+  float* sO = (float*)&vlds[0][0];
+  f32x2* sml = (f32x2*)&klds[0][0];
 #pragma unroll
   for (int nu = 0; nu < 4; nu++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) sO[w][4 * b + i][16 * nu + n] = O[nu][i];
+    for (int i = 0; i < 4; i++) sO[(w * 16 + 4 * b + i) * kMRow + 16 * nu + n] = O[nu][i];
+  if (l < 16) sml[w * 16 + l] = f32x2{mx, lsum};
   __syncthreads();
+  // thread: row r, dims d0 and d0 + 1
   const int r = tid >> 5, d0 = (tid & 31) * 2;
-  float M = sm[0][r];
+  f32x2 ml[kDecWaves];  // (m, l) of row r per wave
 #pragma unroll
-  for (int v = 1; v < kDecWaves; v++) M = __builtin_fmaxf(M, sm[v][r]);
-  float L = 0.f, acc[2] = {0.f, 0.f};
+  for (int v = 0; v < kDecWaves; v++) ml[v] = sml[v * 16 + r];
+  float M = ml[0][0];
+#pragma unroll
+  for (int v = 1; v < kDecWaves; v++) M = __builtin_fmaxf(M, ml[v][0]);
+  float L = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int v = 0; v < kDecWaves; v++) {
-    const float al = __builtin_amdgcn_exp2f(sm[v][r] - M);
-    L = __builtin_fmaf(sl[v][r], al, L);
-#pragma unroll
-    for (int e = 0; e < 2; e++) acc[e] = __builtin_fmaf(sO[v][r][d0 + e], al, acc[e]);
+    const float al = __builtin_amdgcn_exp2f(ml[v][0] - M);
+    L = __builtin_fmaf(ml[v][1], al, L);
+    const f32x2 o2 = *(const f32x2*)(sO + (v * 16 + r) * kMRow + d0);
+    a0 = __builtin_fmaf(o2[0], al, a0);
+    a1 = __builtin_fmaf(o2[1], al, a1);
   }
-  float* p = a.part + ((size_t)(half * 16 + r) * a.nwg + blockIdx.x) * kPart;
-  *(f32x2*)(p + 4 + d0) = f32x2{acc[0], acc[1]};
-  if ((tid & 31) == 0) {
-    p[0] = M;
-    p[1] = L;
-  }
+  float* pp = a.part + ((size_t)(half * 16 + r) * a.nwg + blockIdx.x) * kPart;
+  *(f32x2*)(pp + 4 + d0) = f32x2{a0, a1};
+  if (d0 == 0) *(f32x2*)pp = f32x2{M, L};
 }
 
 // ---------------------------------------------------------------- finish
@@ -337,24 +376,22 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   }
   const uint16_t* qrow = raw ? prep : a.q + (size_t)h * D;
   const uint16_t* knew = raw ? prep + D : (a.knew ? a.knew + (size_t)kvh * D : nullptr);
-  // ---- every load first: partials, then the tail row of this lane
+  // ---- every load first: partials, then the tail row of this lane.  Loads
+  // go out unconditionally (partials beyond nwg and tail rows beyond the
+  // tail read a valid partial / row, and their values are replaced), so no
+  // register is set up or merged on a branch.
   const float* ph = a.part + (size_t)h * a.nwg * kPart;
   float pm[2], pl[2];
   f32x4 po[2][2];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int s = l + 64 * u;
-    if (s < a.nwg) {
-      const float* pp = ph + (size_t)s * kPart;
-      pm[u] = pp[0];
-      pl[u] = pp[1];
-      po[u][0] = *(const f32x4*)(pp + 4 + 8 * c);
-      po[u][1] = *(const f32x4*)(pp + 8 + 8 * c);
-    } else {
-      pm[u] = -1e30f;
-      pl[u] = 0.f;
-      po[u][0] = po[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    const float* pp = ph + (size_t)(s < a.nwg ? s : 0) * kPart;
+    const f32x2 ml = *(const f32x2*)pp;
+    pm[u] = s < a.nwg ? ml[0] : -1e30f;
+    pl[u] = s < a.nwg ? ml[1] : 0.f;
+    po[u][0] = *(const f32x4*)(pp + 4 + 8 * c);
+    po[u][1] = *(const f32x4*)(pp + 8 + 8 * c);
   }
   if constexpr (kPrep) {
     __builtin_amdgcn_sched_barrier(0);
@@ -368,27 +405,25 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     // barrier needed, no wait for the partials' loads)
     __builtin_amdgcn_s_waitcnt(0xC07F);
   }
-  u32x4 kq[8], qq[8], vrow[8], vv = u32x4{0u, 0u, 0u, 0u};
   const bool live = l < ntail;
   // the fresh token completes the group: commit it in this launch
   const bool commit = a.knew && ntail == G;
-  if (live) {
-    const bool fresh = a.knew && l == ntail - 1;
-    const uint16_t* kp = fresh ? knew : a.ktail + ((size_t)l * NKV + kvh) * D;
-    const uint16_t* vp = fresh ? a.vnew + kvh * D : a.vtail + ((size_t)l * NKV + kvh) * D;
-    const uint16_t* qp = qrow;
+  const int trow = live ? l : 0;  // (tail row 0 exists whatever the tail length)
+  const bool fresh = a.knew && l == ntail - 1;
+  const uint16_t* kp = fresh ? knew : a.ktail + ((size_t)trow * NKV + kvh) * D;
+  const uint16_t* vp = fresh ? a.vnew + kvh * D : a.vtail + ((size_t)trow * NKV + kvh) * D;
+  u32x4 kq[8], qq[8], vrow[8];
 #pragma unroll
-    for (int cc = 0; cc < 8; cc++) {
-      kq[cc] = *(const u32x4*)(kp + 8 * cc);
-      qq[cc] = *(const u32x4*)(qp + 8 * cc);
-    }
-    // (this lane's 8 V dims on their own: indexing the full row below with
-    // the runtime c would put it in scratch memory)
-    vv = *(const u32x4*)(vp + 8 * c);
-    if (commit) {
+  for (int cc = 0; cc < 8; cc++) {
+    kq[cc] = *(const u32x4*)(kp + 8 * cc);
+    qq[cc] = *(const u32x4*)(qrow + 8 * cc);
+  }
+  // (this lane's 8 V dims on their own: indexing the full row below with
+  // the runtime c would put it in scratch memory)
+  const u32x4 vv = *(const u32x4*)(vp + 8 * c);
+  if (commit) {
 #pragma unroll
-      for (int cc = 0; cc < 8; cc++) vrow[cc] = *(const u32x4*)(vp + 8 * cc);
-    }
+    for (int cc = 0; cc < 8; cc++) vrow[cc] = *(const u32x4*)(vp + 8 * cc);
   }
   // the fresh token joins the tail, written once per kv head
   if (a.knew && c == 0 && h % GQA == 0 && l < 16) {
@@ -400,17 +435,19 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   // ---- tail scores (log2 units) and this lane's V values (dims 8c..8c+7)
   float x = -1e30f, vf[8];
   if (!commit) {
-    if (live) {
-      float sacc = 0.f;
+    // (pairs taken with shufflevector: a bit_cast of one 32-bit element into
+    // the dot product's f16x2 operand compiled to the same source registers
+    // for all four elements of a 16-byte chunk)
+    float sacc = 0.f;
 #pragma unroll
-      for (int cc = 0; cc < 8; cc++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          sacc = __builtin_fmaf(h2f((uint16_t)qq[cc][i]), h2f((uint16_t)kq[cc][i]), sacc);
-          sacc = __builtin_fmaf(h2f((uint16_t)(qq[cc][i] >> 16)), h2f((uint16_t)(kq[cc][i] >> 16)), sacc);
-        }
-      x = sacc * (a.scale * kLog2e);
+    for (int cc = 0; cc < 8; cc++) {
+      const f16x8 q8 = __builtin_bit_cast(f16x8, qq[cc]), k8 = __builtin_bit_cast(f16x8, kq[cc]);
+      sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 0, 1), __builtin_shufflevector(k8, k8, 0, 1), sacc, false);
+      sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 2, 3), __builtin_shufflevector(k8, k8, 2, 3), sacc, false);
+      sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 4, 5), __builtin_shufflevector(k8, k8, 4, 5), sacc, false);
+      sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 6, 7), __builtin_shufflevector(k8, k8, 6, 7), sacc, false);
     }
+    x = live ? sacc * (a.scale * kLog2e) : -1e30f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       vf[2 * i] = h2f((uint16_t)vv[i]);
