@@ -345,6 +345,42 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   if (d0 == 0) *(f32x2*)pp = f32x2{M, L};
 }
 
+// Wave sums of 8 values by recursive halving: a permlane32 swap pairs value e
+// of the lower half with value 4 + e of the upper half (each side adds its
+// partner's copy of the value it keeps), a permlane16 swap does the same for
+// 4 -> 2 values, a DPP exchange across lane bit 3 for 2 -> 1, and three DPP
+// adds (half-row mirror, quad swaps) finish the 8-lane groups.  Every lane
+// returns the wave total of value halving_dim(lane).
+__device__ __forceinline__ int halving_dim(int lane) {
+  return ((lane >> 3) & 1) + 2 * ((lane >> 4) & 1) + 4 * ((lane >> 5) & 1);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
+                                                               0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum8_halving(const float (&o)[8]) {
+  float s4[4], s2[2];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, o[e]),
+                                                    __builtin_bit_cast(uint32_t, o[4 + e]), false, false);
+    s4[e] = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+  }
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, s4[e]),
+                                                    __builtin_bit_cast(uint32_t, s4[2 + e]), false, false);
+    s2[e] = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+  }
+  const bool hi = (__lane_id() >> 3) & 1;
+  float v = (hi ? s2[1] : s2[0]) + row_ror<8>(hi ? s2[0] : s2[1]);
+  v += dpp_f<0x141>(v);  // row_half_mirror: lane i <- lane 7 - i of its 8
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  return v;
+}
+
 // ---------------------------------------------------------------- finish
 // grid = 256 items (query head h, dims 8c..8c+7), block = 64 (one wave).
 // Workgroups are handed to the 8 XCDs round-robin (XCD = blockIdx.x mod 8),
@@ -533,16 +569,10 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     }
   }
   L = wave_sum_fast(L);
-#pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = wave_sum_fast(o[e]);
-  if (l == 0) {
-    const float inv = 1.f / L;
-    u32x4 r;
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      r[e] = (uint32_t)f2h(o[2 * e] * inv) | ((uint32_t)f2h(o[2 * e + 1] * inv) << 16);
-    *(u32x4*)(a.out + h * D + 8 * c) = r;
-  }
+  // the 8 dims summed by recursive halving: lanes of each 8-lane group end
+  // with dim e(l), one store per group
+  const float oe = wave_sum8_halving(o);
+  if ((l & 7) == 0) a.out[h * D + 8 * c + halving_dim(l)] = f2h(oe * (1.f / L));
 }
 
 }  // namespace cia
