@@ -537,8 +537,9 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
     """H2O eviction decode on one layer: a C-slot per-token FP8 buffer,
     window W, a P-token prompt, then `steps` single-token steps through the
     decode loop (slot choice on the device, no host round trip), timed as a
-    whole; then 64 more steps with events around the placement launch and
-    the two attention launches."""
+    whole; then 64 more steps with events around the scores launch (which
+    also chooses the slot and quantises the token) and the exp + mass
+    launches."""
     import ctypes
     import torch
     from cuda_inf_amd import _lib, workload
@@ -574,19 +575,20 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
     ptrs = (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs])
     loop(P + steps, extra, ptrs)
     torch.cuda.synchronize()
-    place = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) * 1e3 for i in range(extra))
-    attn = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) * 1e3 for i in range(extra))
+    scores = sorted(evs[3 * i].elapsed_time(evs[3 * i + 1]) * 1e3 for i in range(extra))
+    rest = sorted(evs[3 * i + 1].elapsed_time(evs[3 * i + 2]) * 1e3 for i in range(extra))
     # per step: FP8 K+V and fp16 scales of every live slot, its position
     # and mass (read + write), q in, out written
     step_bytes = C * (2 * NKV * D + 2 * NKV * 2 + 4 + 8) + 2 * NH * D * 2
     res = {"slots": C, "window": W, "prompt": P, "steps": steps, "us_per_step": round(us, 2),
            "gbps": round(step_bytes / (us * 1e-6) / 1e9, 1),
-           "place_us_median": round(place[extra // 2], 2),
-           "attention_us_median": round(attn[extra // 2], 2),
+           "scores_place_us_median": round(scores[extra // 2], 2),
+           "exp_mass_us_median": round(rest[extra // 2], 2),
            "evictions": steps + extra + P - C,
-           "policy": "device slot choice (cia_h2o_place), no host round trip"}
-    log(f"h2o C={C} W={W}: {us:.2f} us/step over {steps} steps; place {res['place_us_median']} us,"
-        f" attention {res['attention_us_median']} us (medians)")
+           "policy": "slot choice and quantisation inside the scores launch (3 launches per "
+                     "step, no host round trip)"}
+    log(f"h2o C={C} W={W}: {us:.2f} us/step over {steps} steps; scores + placement "
+        f"{res['scores_place_us_median']} us, exp + mass {res['exp_mass_us_median']} us (medians)")
     return res
 
 

@@ -38,6 +38,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "h2o_place.h"
 
 namespace cia {
 
@@ -58,6 +59,37 @@ struct H2oArgs {
   float* part_ml;  // [Sq][32][nblk][2]: block max, block sum
   int n_live, nblk, qpos0, Sq;
   float scale;
+  // single-token step that evicted a slot (placement in the scores launch):
+  // the slot (read from *placed), whose mass restarts from 0 and whose
+  // position becomes posj in the mass launch; null otherwise
+  const int32_t* placed;
+  int32_t* slotpos_w;
+  int posj;
+};
+
+// Placement of a single fresh token inside the scores launch (the
+// reference's host loop, engine.cu:808-826, for one token).  Every
+// workgroup derives the same slot: n0 while the buffer fills, else the
+// minimum (mass, slot) key outside the window, else over all slots -- the
+// rule of k_h2o_place.  Masses and positions are only read in this launch,
+// so every workgroup sees the same values: the evicted slot's mass reset
+// and new position are written by the mass launch (the position cannot
+// change eligibility within the step: old and new positions are both <=
+// the query's).  The workgroup whose 64-slot block holds the slot quantises
+// the token for its kv head (engine.cu:317-333), writes the bytes and
+// scales, and uses them in place of the slot's old ones; for a filling slot
+// it also writes the position.
+struct H2oPlace {
+  const uint16_t* k;  // the token's K and V [8][64] fp16
+  const uint16_t* v;
+  uint8_t* kf;
+  uint8_t* vf;
+  uint16_t* ks;
+  uint16_t* vs;
+  const float* attn;
+  int32_t* slotpos;
+  int32_t* dst;  // dst[0] = the slot, -1 when none can be taken
+  int n0, C, W, posj;
 };
 
 __device__ __forceinline__ int wave_id() {
@@ -66,14 +98,47 @@ __device__ __forceinline__ int wave_id() {
 
 // grid = (nblk, 8, Sq), block = 256 (wave w: query head 4 kvh + w).  All
 // global loads are issued before the first use, so the kernel waits on
-// memory once.
-__global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a) {
-  __shared__ uint8_t vl[64 * D];  // V rows of the block's slots, this kv head
+// memory once.  kPlace (Sq = 1): the token is placed here (H2oPlace).
+template <bool kPlace>
+__global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
+  __shared__ __attribute__((aligned(16))) uint8_t vl[64 * D];  // V rows of the block's slots, this kv head
+  __shared__ __attribute__((aligned(16))) uint8_t newkv[2][D];  // kPlace: the token's K / V bytes
+  __shared__ uint16_t newsc[2];
+  __shared__ uint64_t red[2][4];
   const int blk = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, h = kvh * GQA + wave_id();
   const int qpos = a.qpos0 + i, t0 = blk * 64, t = t0 + lane;
   const int row = tid >> 2, c4 = tid & 3;
   const bool live = t < a.n_live;
+  // ---- placement loads first: the token's row of this kv head, masses
+  // and positions (each thread 8 slots of a 2048-slot buffer)
+  int slot = -1;
+  float tk = 0.f, tv = 0.f;
+  uint64_t kwin = ~0ull, kall = ~0ull;
+  if constexpr (kPlace) {
+    tk = h2f(pl.k[kvh * D + lane]);
+    tv = h2f(pl.v[kvh * D + lane]);
+    if (pl.n0 >= pl.C) {
+      const int lim = pl.posj - pl.W;
+      for (int u0 = tid; u0 < pl.C; u0 += 256 * 8) {
+        float m[8];
+        int sp[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int u = u0 + 256 * e;
+          m[e] = u < pl.C ? pl.attn[u] : kPicked;
+          sp[e] = u < pl.C ? a.slot_pos[u] : 0;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          if (m[e] < kPicked) {
+            const uint64_t key = place_key(m[e], u0 + 256 * e);
+            kall = min_u64(kall, key);
+            if (sp[e] <= lim) kwin = min_u64(kwin, key);
+          }
+      }
+    }
+  }
   const u32x4* qp = (const u32x4*)(a.q + ((size_t)i * NH + h) * D);
   u32x4 qv[8];
 #pragma unroll
@@ -91,6 +156,58 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a) {
     const u32x4* kp = (const u32x4*)(a.kf + ((size_t)t * NKV + kvh) * D);
 #pragma unroll
     for (int c = 0; c < 4; c++) kr[c] = kp[c];
+  }
+  if constexpr (kPlace) {
+    // ---- the slot (the same in every workgroup)
+    if (pl.n0 < pl.C) {
+      slot = pl.n0;
+    } else {
+      kwin = wave_min_u64(kwin);
+      kall = wave_min_u64(kall);
+      if (lane == 0) {
+        red[0][wave_id()] = kwin;
+        red[1][wave_id()] = kall;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        kwin = min_u64(kwin, red[0][w]);
+        kall = min_u64(kall, red[1][w]);
+      }
+      const uint64_t kb = kwin != ~0ull ? kwin : kall;
+      slot = kb != ~0ull ? (int)(uint32_t)kb : -1;
+    }
+    if (blk == 0 && kvh == 0 && tid == 0) pl.dst[0] = slot;
+    if (slot >= t0 && slot < t0 + 64) {
+      // this block holds the slot: quantise the token's kv head (wave 0),
+      // write it, and use it for the slot's key, value and scales
+      if (wave_id() == 0) {
+        const float sck = quant_scale(wave_max_fast(__builtin_fabsf(tk)));
+        const float scv = quant_scale(wave_max_fast(__builtin_fabsf(tv)));
+        const uint32_t kb = e4m3x2(tk / sck, 0.f) & 0xFFu, vb = e4m3x2(tv / scv, 0.f) & 0xFFu;
+        newkv[0][lane] = (uint8_t)kb;
+        newkv[1][lane] = (uint8_t)vb;
+        const size_t o = ((size_t)slot * NKV + kvh) * D + lane;
+        pl.kf[o] = (uint8_t)kb;
+        pl.vf[o] = (uint8_t)vb;
+        if (lane == 0) {
+          newsc[0] = f2h(sck);
+          newsc[1] = f2h(scv);
+          pl.ks[slot * NKV + kvh] = newsc[0];
+          pl.vs[slot * NKV + kvh] = newsc[1];
+          if (kvh == 0 && pl.n0 < pl.C) pl.slotpos[slot] = pl.posj;
+        }
+      }
+      __syncthreads();
+      if (t == slot) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) kr[c] = *(const u32x4*)(newkv[0] + 16 * c);
+        ks16 = newsc[0];
+        vs16 = newsc[1];
+        sp = pl.posj;
+      }
+      if (t0 + row == slot) vst = *(const u32x4*)(newkv[1] + 16 * c4);
+    }
   }
   *(u32x4*)(vl + row * D + c4 * 16) = vst;
   const bool ok = live && sp <= qpos;
@@ -203,8 +320,9 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
   __syncthreads();
   const int t = blockIdx.x * 1024 + tid;
   if (t >= a.n_live) return;
-  const int sp = a.slot_pos[t];
-  float acc = a.attn_sum[t];
+  const bool re = a.placed && t == *a.placed;  // the slot evicted by this step
+  const int sp = re ? a.posj : a.slot_pos[t];
+  float acc = re ? 0.0f : a.attn_sum[t];
   for (int i = 0; i < a.Sq; i++) {
     if (sp > a.qpos0 + i) continue;
     float ev[NH];
@@ -214,6 +332,7 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
     for (int h = 0; h < NH; h++) acc = acc + ev[h] * inv[i * NH + h];
   }
   a.attn_sum[t] = acc;
+  if (re) a.slotpos_w[t] = a.posj;
 }
 
 int64_t h2o_ws_bytes(int S, int C) {
@@ -263,7 +382,10 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     a.qpos0 = past + c0;
     a.Sq = sq;
     a.scale = scale;
-    hipLaunchKernelGGL(k_h2o_scores, dim3(nblk, NKV, sq), dim3(256), 0, s, a);
+    a.placed = nullptr;
+    a.slotpos_w = nullptr;
+    a.posj = 0;
+    hipLaunchKernelGGL(k_h2o_scores<false>, dim3(nblk, NKV, sq), dim3(256), 0, s, a, H2oPlace{});
     int st = launch_status();
     if (st) return st;
     hipLaunchKernelGGL(k_h2o_exp, dim3(nblk, NKV, sq), dim3(256), 0, s, a);
@@ -271,5 +393,70 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     hipLaunchKernelGGL(k_h2o_mass, dim3((n_live + 1023) / 1024), dim3(1024), 0, s, a);
     if ((st = launch_status())) return st;
   }
+  return CIA_OK;
+}
+
+// One decode step of an H2O layer in three launches: the token placed and
+// quantised inside the scores launch (H2oPlace), then exp and mass.  The
+// same slots, positions, bytes and masses as cia_h2o_place followed by
+// cia_attention_h2o for S = 1.  mid_event (may be NULL) is recorded after
+// the scores launch.
+extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
+    const uint16_t* q, const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
+    uint16_t* ks, uint16_t* vs, float* attn_sum, int32_t* slot_pos, int32_t* dst_slots,
+    int* n_live, int C, int W, int past, uint16_t* out, float scale, void* ws, int64_t ws_bytes,
+    void* stream, void* mid_event) {
+  CIA_REQUIRE(n_live, CIA_ERR_NULL);
+  CIA_REQUIRE(past >= 0 && C >= 1 && W >= 0 && *n_live >= 0 && *n_live <= C, CIA_ERR_ARG);
+  CIA_REQUIRE(q && k && v && kf && vf && ks && vs && attn_sum && slot_pos && dst_slots && out && ws,
+              CIA_ERR_NULL);
+  const int n0 = *n_live, n1 = n0 < C ? n0 + 1 : C;
+  CIA_REQUIRE(ws_bytes >= h2o_ws_bytes(1, n1), CIA_ERR_ARG);
+  CIA_REQUIRE(aligned(q, 16) && aligned(kf, 16) && aligned(vf, 16) && aligned(ws, 16) &&
+                  aligned(ks, 2) && aligned(vs, 2) && aligned(out, 2) && aligned(attn_sum, 4) &&
+                  aligned(slot_pos, 4) && aligned(dst_slots, 4) && aligned(k, 2) && aligned(v, 2),
+              CIA_ERR_ALIGN);
+  hipStream_t s = (hipStream_t)stream;
+  const int nblk = (n1 + 63) / 64;
+  H2oArgs a;
+  a.q = q;
+  a.kf = kf;
+  a.vf = vf;
+  a.ks = ks;
+  a.vs = vs;
+  a.slot_pos = slot_pos;
+  a.out = out;
+  a.attn_sum = attn_sum;
+  a.sc = (float*)ws;
+  a.part_o = a.sc + (size_t)NH * nblk * 64;
+  a.part_ml = a.part_o + (size_t)NH * nblk * 64;
+  a.n_live = n1;
+  a.nblk = nblk;
+  a.qpos0 = past;
+  a.Sq = 1;
+  a.scale = scale;
+  a.placed = nullptr;
+  a.slotpos_w = nullptr;
+  a.posj = past;
+  const H2oPlace pl{k, v, kf, vf, ks, vs, attn_sum, slot_pos, dst_slots, n0, C, W, past};
+  hipLaunchKernelGGL(k_h2o_scores<true>, dim3(nblk, NKV, 1), dim3(256), 0, s, a, pl);
+  int st = launch_status();
+  if (st) return st;
+  if (mid_event) {
+    const hipError_t e = hipEventRecord((hipEvent_t)mid_event, s);
+    if (e != hipSuccess) {
+      set_hip_error(e);
+      return CIA_ERR_HIP;
+    }
+  }
+  hipLaunchKernelGGL(k_h2o_exp, dim3(nblk, NKV, 1), dim3(256), 0, s, a);
+  if ((st = launch_status())) return st;
+  if (n0 >= C) {
+    a.placed = dst_slots;
+    a.slotpos_w = slot_pos;
+  }
+  hipLaunchKernelGGL(k_h2o_mass, dim3((n1 + 1023) / 1024), dim3(1024), 0, s, a);
+  if ((st = launch_status())) return st;
+  *n_live = n1;
   return CIA_OK;
 }

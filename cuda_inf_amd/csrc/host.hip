@@ -21,6 +21,12 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
     int64_t ws_bytes, void* stream, void* mid_event, const void* prep);
 
+extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
+    const uint16_t* q, const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
+    uint16_t* ks, uint16_t* vs, float* attn_sum, int32_t* slot_pos, int32_t* dst_slots,
+    int* n_live, int C, int W, int past, uint16_t* out, float scale, void* ws, int64_t ws_bytes,
+    void* stream, void* mid_event);
+
 extern "C" __attribute__((visibility("hidden"))) int cia_qk_prep_into(
     const uint16_t* q, const uint16_t* k, const uint16_t* qw, const uint16_t* kw, uint16_t* oq,
     uint16_t* ok, int pos0, int S, float eps, float theta, void* stream);
@@ -187,14 +193,23 @@ int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16
   const int n0 = L->n_live;
   int st = prep_qk(L, q, k, S, past, stream);
   if (st) return st;
-  st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
-                         &L->n_live, C, L->window, S, past, stream);
-  if (st) return st;
-  if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
-    return st;
-  st = cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out, L->hattn,
-                         S, past, scale, L->ws_mass, cia_h2o_workspace_bytes(S, C), stream);
-  if (st) return st;
+  if (S == 1) {
+    // one token: placed and quantised inside the attention's first launch
+    st = cia_h2o_decode_step(q, k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos,
+                             L->d_dst, &L->n_live, C, L->window, past, out, scale, L->ws_mass,
+                             cia_h2o_workspace_bytes(1, C), stream, mid_event);
+    if (st) return st;
+  } else {
+    st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
+                       &L->n_live, C, L->window, S, past, stream);
+    if (st) return st;
+    if (mid_event && (st = hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream))))
+      return st;
+    st = cia_attention_h2o(q, L->kf, L->vf, L->ks, L->vs, L->d_slotpos, L->n_live, out,
+                           L->hattn, S, past, scale, L->ws_mass, cia_h2o_workspace_bytes(S, C),
+                           stream);
+    if (st) return st;
+  }
   // the last token evicted iff it found no free slot
   if (evicted && n0 + S > C) {
     int32_t slot = -1;

@@ -5,6 +5,7 @@
 // bit-exact: amax is an order-free max, the scale is amax/448 + 1e-12 with
 // an IEEE division, the bytes are encoded from x / scale (fp32) and the
 // stored scale is fp16(scale).
+#include "h2o_place.h"
 #include <algorithm>
 
 #include "common.h"
@@ -232,21 +233,6 @@ __global__ __launch_bounds__(64) void k_quant_write(const uint16_t* __restrict__
 // quantised into their slots here.
 constexpr int kPlaceThreads = 1024;
 constexpr int kPlaceFuse = 16;
-constexpr float kPicked = 1e30f;
-
-__device__ __forceinline__ uint64_t place_key(float a, int t) {
-  uint32_t b = __float_as_uint(a == 0.0f ? 0.0f : a);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // float order as unsigned order
-  return ((uint64_t)b << 32) | (uint32_t)t;
-}
-
-__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return b < a ? b : a; }
-
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = min_u64(x, __shfl_xor(x, off));
-  return x;
-}
 
 __global__ __launch_bounds__(kPlaceThreads) void k_h2o_place(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint8_t* __restrict__ kf,
