@@ -92,8 +92,8 @@ def test_decode_nsplit_sweep(orc, cia, dev, nsplit):
     assert np.all(pm.cpu().numpy()[empty] == np.float32(-1e30))
 
 
-# 65540 and 131080 keys: 2 and 4 pairs per wave (several pairs per wave;
-# the smaller sizes have at most one)
+# 65540 and 131080 keys: 2 and 4 pairs per wave; below 32768 keys a wave
+# has at most one pair (33000: a few waves take two)
 @pytest.mark.parametrize("ntok", [1, 63, 64, 65, 127, 128, 129, 255, 256, 257, 2032, 5000, 33000,
                                   65540, 131080])
 def test_decode_matrix_cores(orc, cia, dev, ntok):
