@@ -305,15 +305,19 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
   for (int pr = w; pr < a.Sq * NH; pr += 16) {
     const float* e = a.sc + pr * cp;
     float acc = 0.0f;
-    int t = lane;
-    for (; t + 64 * 15 < a.n_live; t += 64 * 16) {
-      float v[16];
+    // 2048 slots per round, all 32 loads of a lane issued before its adds
+    // (slots past n_live add +0, which leaves the sum's bits unchanged: the
+    // numerators are never -0)
+    for (int t0 = 0; t0 < a.n_live; t0 += 64 * 32) {
+      float v[32];
 #pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = e[t + 64 * u];
+      for (int u = 0; u < 32; u++) {
+        const int t = t0 + lane + 64 * u;
+        v[u] = t < a.n_live ? e[t] : 0.0f;
+      }
 #pragma unroll
-      for (int u = 0; u < 16; u++) acc = acc + v[u];
+      for (int u = 0; u < 32; u++) acc = acc + v[u];
     }
-    for (; t < a.n_live; t += 64) acc = acc + e[t];
     const float l = wave_sum(acc);  // the butterfly of the rule
     if (lane == 0) inv[pr] = 1.0f / l;
   }
