@@ -22,12 +22,15 @@ def _u16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def test_h2o_small_stepwise(orc, cia, dev):
-    """C=128, W=16, 64-token prompt, 300 decode steps: every step checked."""
+# (C, W, prompt, steps, seed): a partial last 64-slot block (50 slots) and a
+# window of 5 in the second case
+@pytest.mark.parametrize("C,W,P,N,seed", [(128, 16, 64, 300, 21), (50, 5, 20, 120, 22)])
+def test_h2o_small_stepwise(orc, cia, dev, C, W, P, N, seed):
+    """Single-token decode steps after a prompt, every step checked: the
+    evicted slot, attn_sum bits, positions and outputs."""
     from cuda_inf_amd.layer import AttnLayer
     from cuda_inf_amd.workload import qkv
-    C, W, P, N = 128, 16, 64, 300
-    q, k, v = qkv(P + N, seed=21, device="cpu", prep=False)
+    q, k, v = qkv(P + N, seed=seed, device="cpu", prep=False)
     qn, kn, vn = _u16(q), _u16(k), _u16(v)
     L = AttnLayer(P + N + 4, budget=C, window=W, prompt_len=P, max_batch=P, device=dev)
     assert (L.budget, L.window) == (C, W)
