@@ -86,6 +86,8 @@ struct DecodeArgs {
   uint16_t* out;  // [32][64]
   QkPrep prep;    // prep.qw != null: q and the fresh k arrive raw and are
                   // normalised and rotated here (engine.cu:799-801)
+  uint16_t* prepq;  // with prep: the prepared q [32][64] and fresh k [8][64]
+                    // rows, written by the attend for the finish
 };
 
 // ---------------------------------------------------------------- attend
@@ -118,14 +120,24 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   // per wave measurably slow the K/V stream behind them).  Raw q (with the
   // QK producers) is loaded first too, but normalised and rotated while the
   // first pair's K/V loads are in flight.
-  uint32_t qraw[2] = {0u, 0u}, wraw = 0u;
+  uint32_t qraw[4] = {0u, 0u, 0u, 0u}, wraw = 0u, kraw = 0u, wkraw = 0u;
   u32x4 qrow2[2];
   float invf = 0.0f;
   if constexpr (kPrep) {
+    // (every wave loads four raw q rows, rows 4 (w mod 4) + r of the half,
+    // and the fresh raw k row of kv head 4 half + (w mod 4); waves 0-3 use
+    // them)
     invf = a.prep.rt.invf[l & 31];
     wraw = a.prep.qw[l];
 #pragma unroll
-    for (int r = 0; r < 2; r++) qraw[r] = a.q[(size_t)(half * 16 + 2 * w + r) * D + l];
+    for (int r = 0; r < 4; r++)
+      qraw[r] = a.q[(size_t)(half * 16 + 4 * (w & 3) + r) * D + l];
+    // (unconditional: a load under a branch makes the wave wait for it at
+    // the join, before the pair's loads are issued; without a fresh k the
+    // row is a q row and unused)
+    const uint16_t* kn = a.knew ? a.knew : a.q;
+    kraw = kn[(size_t)(half * 4 + (w & 3)) * D + l];
+    wkraw = a.prep.kw[l];
   } else {
 #pragma unroll
     for (int r = 0; r < 2; r++)
@@ -165,49 +177,57 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_decode_attend(DecodeArgs a) 
   // in two phases per workgroup: waves 0-3, a barrier, then waves 4-7.  With
   // every wave's loads issued at once, each wave's last bytes land at the
   // end of the launch and all arithmetic queues behind them; staggered,
-  // the first half computes while the second half streams in.  With the QK
-  // producers the workgroup meets at a barrier anyway, and all waves issue
-  // at once.
+  // the first half computes while the second half streams in.
   {
     const bool cache = p0 < p1 || a.npairs > 0;
     const int pf = p0 < p1 ? p0 : 0;
     const uint8_t* k8 = cache ? a.kc8 : (const uint8_t*)a.ktail;
     const uint8_t* v8 = cache ? a.vc8 : (const uint8_t*)a.vtail;
-    if constexpr (kPrep) {
-      load_k(pf, k8);
-      load_v(pf, v8);
-    } else {
-      // One load in straight-line code, the barrier on either side of it by
-      // wave (each wave executes one barrier; the hardware counts arrivals).
-      // Loads under two conditional branches would merge at the joins into a
-      // conservative count, and every later wait on a pair register would
-      // become a wait for all of the wave's loads.
-      if (w >= kDecWaves / 2) __builtin_amdgcn_s_barrier();
-      load_k(pf, k8);
-      load_v(pf, v8);
-      if (w < kDecWaves / 2) __builtin_amdgcn_s_barrier();
+    // One load in straight-line code, the barrier on either side of it by
+    // wave (each wave executes one barrier; the hardware counts arrivals).
+    // Loads under two conditional branches would merge at the joins into a
+    // conservative count, and every later wait on a pair register would
+    // become a wait for all of the wave's loads.
+    if (w >= kDecWaves / 2) __builtin_amdgcn_s_barrier();
+    load_k(pf, k8);
+    load_v(pf, v8);
+    if (w < kDecWaves / 2) {
+      if constexpr (kPrep) {
+        // The QK producers: waves 0-3 prepare the half's 16 q rows (four
+        // each) while their pair streams in (their raw rows were loaded
+        // ahead of it), and before the barrier, so the rows are in LDS for
+        // every wave after it.  Workgroup 0 of the half also prepares the
+        // fresh k rows of the half's kv heads (one per wave) and stores
+        // both for the finish launch.
+        // (keeps the producers' arithmetic behind the pair's loads, so it
+        // waits only for its own older loads)
+        __builtin_amdgcn_sched_barrier(0);
+        float sn, cs;
+        rope_sincos_f(invf, a.qpos, sn, cs);
+        const float wq = h2f((uint16_t)wraw);
+        uint16_t* qrows = (uint16_t*)qb;
+        uint16_t qp[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          qp[r] = qk_norm_rope_sc(h2f((uint16_t)qraw[r]), wq, l, sn, cs, a.prep.eps);
+          qrows[(4 * w + r) * D + l] = qp[r];
+        }
+        if (w == 0 && l < 8) *(u32x4*)(qb + kQRowsB + 16 * l) = u32x4{0u, 0u, 0u, 0u};
+        if (blockIdx.x == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) a.prepq[(size_t)(half * 16 + 4 * w + r) * D + l] = qp[r];
+          if (a.knew)
+            a.prepq[(size_t)(NH + half * 4 + w) * D + l] = qk_norm_rope_sc(
+                h2f((uint16_t)kraw), h2f((uint16_t)wkraw), l, sn, cs, a.prep.eps);
+        }
+        // LDS writes done, then the barrier alone: a full __syncthreads
+        // would also wait for the pair's K/V loads
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      }
+      __builtin_amdgcn_s_barrier();
     }
   }
-  if constexpr (kPrep) {
-    // (keeps the producers' arithmetic behind the first pair's loads, so it
-    // waits only for its own older loads)
-    __builtin_amdgcn_sched_barrier(0);
-    // the QK producers on the half's 16 query heads: two per wave, one dim
-    // per lane, into LDS; wave 0 also writes the zero bytes
-    float sn, cs;
-    rope_sincos_f(invf, a.qpos, sn, cs);
-    const float wq = h2f((uint16_t)wraw);
-    uint16_t* qrows = (uint16_t*)qb;
-#pragma unroll
-    for (int r = 0; r < 2; r++)
-      qrows[(2 * w + r) * D + l] =
-          qk_norm_rope_sc(h2f((uint16_t)qraw[r]), wq, l, sn, cs, a.prep.eps);
-    if (w == 0 && l < 8) *(u32x4*)(qb + kQRowsB + 16 * l) = u32x4{0u, 0u, 0u, 0u};
-    // LDS writes done, then the barrier alone: a full __syncthreads would
-    // also wait for the first pair's K/V loads
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-  } else {
+  if constexpr (!kPrep) {
     // (one wave writes and reads its own copy: LDS executes a wave's
     // instructions in order, the wave barrier keeps the compiler from
     // reordering them)
@@ -388,30 +408,13 @@ __device__ __forceinline__ float wave_sum8_halving(const float (&o)[8]) {
 // 8 items of a head -- and the 4 heads of one kv head -- share an XCD and
 // read that head's partials and tail rows through one L2.  Lane s holds FP8
 // partials s and s + 64; lane t attends tail key committed + t.
-template <bool kPrep>
 __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
   const int j = blockIdx.x >> 3;
   const int h = (blockIdx.x & 7) * 4 + (j >> 3), c = j & 7, kvh = h / GQA;
   const int l = threadIdx.x;
   const int ntail = a.qpos + 1 - a.committed;  // 0..64
-  // with the QK producers: this head's raw q row and the fresh raw k row
-  // (one dim per lane) are loaded first and prepared while the partials
-  // load
-  __shared__ __attribute__((aligned(16))) uint16_t prep[2 * D];
-  constexpr bool raw = kPrep;
-  uint32_t qraw = 0u, kraw = 0u, wq = 0u, wk = 0u;
-  float invf = 0.0f;
-  if constexpr (kPrep) {
-    invf = a.prep.rt.invf[l & 31];
-    qraw = a.q[(size_t)h * D + l];
-    wq = a.prep.qw[l];
-    if (a.knew) {
-      kraw = a.knew[(size_t)kvh * D + l];
-      wk = a.prep.kw[l];
-    }
-  }
-  const uint16_t* qrow = raw ? prep : a.q + (size_t)h * D;
-  const uint16_t* knew = raw ? prep + D : (a.knew ? a.knew + (size_t)kvh * D : nullptr);
+  const uint16_t* qrow = a.q + (size_t)h * D;
+  const uint16_t* knew = a.knew ? a.knew + (size_t)kvh * D : nullptr;
   // ---- every load first: partials, then the tail row of this lane.  Loads
   // go out unconditionally (partials beyond nwg and tail rows beyond the
   // tail read a valid partial / row, and their values are replaced), so no
@@ -428,18 +431,6 @@ __global__ __launch_bounds__(64) void k_decode_finish(DecodeArgs a) {
     pl[u] = s < a.nwg ? ml[1] : 0.f;
     po[u][0] = *(const f32x4*)(pp + 4 + 8 * c);
     po[u][1] = *(const f32x4*)(pp + 8 + 8 * c);
-  }
-  if constexpr (kPrep) {
-    __builtin_amdgcn_sched_barrier(0);
-    float sn, cs;
-    rope_sincos_f(invf, a.qpos, sn, cs);
-    prep[l] = qk_norm_rope_sc(h2f((uint16_t)qraw), h2f((uint16_t)wq), l, sn, cs, a.prep.eps);
-    if (a.knew)
-      prep[D + l] =
-          qk_norm_rope_sc(h2f((uint16_t)kraw), h2f((uint16_t)wk), l, sn, cs, a.prep.eps);
-    // one wave: the LDS writes are complete once lgkmcnt reaches 0 (no
-    // barrier needed, no wait for the partials' loads)
-    __builtin_amdgcn_s_waitcnt(0xC07F);
   }
   const bool live = l < ntail;
   // the fresh token completes the group: commit it in this launch
@@ -599,7 +590,10 @@ static int dec_nwg(int npairs) {
 
 extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
   if (max_tokens < 0) return 0;
-  return (int64_t)NH * kMaxWgPerHalf * kPart * (int64_t)sizeof(float);
+  // partials, then the prepared q / fresh k rows of a step with the QK
+  // producers inside
+  return (int64_t)NH * kMaxWgPerHalf * kPart * (int64_t)sizeof(float) +
+         (int64_t)(NH + NKV) * D * (int64_t)sizeof(uint16_t);
 }
 
 // Flash-decoding with the library's split and, when knew/vnew are given, the
@@ -616,8 +610,15 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   const int nwg = dec_nwg(npairs);
   if ((int64_t)NH * nwg * kPart * (int64_t)sizeof(float) > ws_bytes) return CIA_ERR_ARG;
   DecodeArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail, knew, vnew, committed, qpos, scale,
-                (float*)ws, npairs, nwg, out, QkPrep{}};
-  if (prep) da.prep = *(const QkPrep*)prep;
+                (float*)ws, npairs, nwg, out, QkPrep{}, nullptr};
+  if (prep) {
+    // the prepared q and fresh k rows follow the partials
+    constexpr int64_t kRowsB = (int64_t)(NH + NKV) * D * sizeof(uint16_t);
+    const int64_t off = (int64_t)NH * nwg * kPart * (int64_t)sizeof(float);
+    if (off + kRowsB > ws_bytes) return CIA_ERR_ARG;
+    da.prep = *(const QkPrep*)prep;
+    da.prepq = (uint16_t*)((char*)ws + off);
+  }
   hipStream_t s = (hipStream_t)stream;
   if (da.prep.qw)
     hipLaunchKernelGGL(k_decode_attend<true>, dim3(nwg, 2), dim3(64 * kDecWaves), 0, s, da);
@@ -632,9 +633,11 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
       return CIA_ERR_HIP;
     }
   }
-  if (da.prep.qw)
-    hipLaunchKernelGGL(k_decode_finish<true>, dim3(kItems), dim3(64), 0, s, da);
-  else
-    hipLaunchKernelGGL(k_decode_finish<false>, dim3(kItems), dim3(64), 0, s, da);
+  if (da.prep.qw) {
+    // the finish reads the rows the attend prepared
+    da.q = da.prepq;
+    if (da.knew) da.knew = da.prepq + NH * D;
+  }
+  hipLaunchKernelGGL(k_decode_finish, dim3(kItems), dim3(64), 0, s, da);
   return launch_status();
 }

@@ -157,7 +157,9 @@ int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                     const uint16_t* ktail, const uint16_t* vtail,
                     int committed, int qpos, float scale, uint16_t* out,
                     void* ws, int64_t ws_bytes, void* stream);
-/* scratch bytes cia_attn_decode needs for contexts of up to max_tokens */
+/* scratch bytes cia_attn_decode needs for contexts of up to max_tokens
+ * (the same buffer as a layer's ws_decode also holds the prepared q and
+ * fresh k rows, 5 KiB, of a decode step that runs the QK producers) */
 int64_t cia_decode_workspace_bytes(int max_tokens);
 
 /* ------------------------------------------------------------------ */
