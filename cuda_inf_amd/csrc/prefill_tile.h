@@ -70,10 +70,14 @@ __device__ __forceinline__ void pf_load8(const PrefillArgs& a, int g, int j, int
   const int kkey = tid >> 3, kch = tid & 7, kp = tid & 31, dc = tid >> 5;
   st.ks = a.ksc[j * NKV + g];
   st.vs = a.vsc[j * NKV + g];
-  st.k = *(const u32x2*)(a.kc8 + ((size_t)(64 * j + kkey) * NKV + g) * D + 8 * kch);
-  const size_t v0 = (size_t)(64 * j + 2 * kp) * NKV + g;
-  st.v0 = *(const uint32_t*)(a.vc8 + v0 * D + 4 * dc);
-  st.v1 = *(const uint32_t*)(a.vc8 + (v0 + NKV) * D + 4 * dc);
+  // the group's rows from a uniform base, this thread's bytes at a 32-bit
+  // offset (one address register per load)
+  const uint8_t* kg = a.kc8 + (size_t)j * (64 * NKV * D);
+  const uint8_t* vg = a.vc8 + (size_t)j * (64 * NKV * D);
+  st.k = *(const u32x2*)(kg + (uint32_t)((kkey * NKV + g) * D + 8 * kch));
+  const uint32_t v0 = (uint32_t)((2 * kp * NKV + g) * D + 4 * dc);
+  st.v0 = *(const uint32_t*)(vg + v0);
+  st.v1 = *(const uint32_t*)(vg + v0 + NKV * D);
 }
 
 // tail rows 0..nvalid-1 (keys committed..); the others stage as zeros
