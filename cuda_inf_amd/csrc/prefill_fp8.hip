@@ -70,11 +70,14 @@ struct F8Stage {
 
 __device__ __forceinline__ void f8_load(const PrefillArgs& a, int g, int j, int tid,
                                         F8Stage& st) {
-  const size_t row = ((size_t)(64 * j + (tid >> 3)) * NKV + g) * D + 8 * (tid & 7);
+  // the group's rows from a uniform base, this thread's bytes at a 32-bit
+  // offset (one address register per load)
+  const size_t grp = (size_t)j * (64 * NKV * D);
+  const uint32_t row = (uint32_t)(((tid >> 3) * NKV + g) * D + 8 * (tid & 7));
   st.ks = a.ksc[j * NKV + g];
   st.vs = a.vsc[j * NKV + g];
-  st.k = *(const u32x2*)(a.kc8 + row);
-  st.v = *(const u32x2*)(a.vc8 + row);
+  st.k = *(const u32x2*)(a.kc8 + grp + row);
+  st.v = *(const u32x2*)(a.vc8 + grp + row);
 }
 
 __device__ __forceinline__ void f8_store(uint8_t* buf, int tid, u32x2 k, u32x2 v) {
