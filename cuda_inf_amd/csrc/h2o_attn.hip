@@ -297,37 +297,59 @@ __global__ __launch_bounds__(256) void k_h2o_exp(H2oArgs a) {
 
 // grid = ceil(n_live / 1024), block = 1024: every block derives 1/l of
 // every (query, head) of the chunk (the same bits), then owns 1024 slots.
-// Loads are batched ahead of the in-order sums.
+// Loads are batched ahead of the in-order sums: a wave's two (query, head)
+// rows pr and pr + 16 load together, and the first query's numerators of
+// the thread's slot are loaded before the normalisers are summed.
 __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
   __shared__ float inv[kChunk * NH];
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const size_t cp = (size_t)a.nblk * 64;
-  for (int pr = w; pr < a.Sq * NH; pr += 16) {
-    const float* e = a.sc + pr * cp;
-    float acc = 0.0f;
-    // 2048 slots per round, all 32 loads of a lane issued before its adds
+  const int t = blockIdx.x * 1024 + tid;
+  const int tc = t < a.n_live ? t : 0;  // (slot 0 exists whenever a block runs)
+  float ev0[NH];
+#pragma unroll
+  for (int h = 0; h < NH; h++) ev0[h] = a.sc[(size_t)h * cp + tc];
+  const int npr = a.Sq * NH;
+  for (int pr = w; pr < npr; pr += 32) {
+    // rows pr and pr + 16 (the second one only when it exists; its loads
+    // then read row pr again and its sum is discarded)
+    const bool two = pr + 16 < npr;
+    const float* e0 = a.sc + pr * cp;
+    const float* e1 = a.sc + (two ? pr + 16 : pr) * cp;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    // 2048 slots per round, all loads of a lane issued before its adds
     // (slots past n_live add +0, which leaves the sum's bits unchanged: the
     // numerators are never -0)
     for (int t0 = 0; t0 < a.n_live; t0 += 64 * 32) {
-      float v[32];
+      float v0[32], v1[32];
 #pragma unroll
       for (int u = 0; u < 32; u++) {
-        const int t = t0 + lane + 64 * u;
-        v[u] = t < a.n_live ? e[t] : 0.0f;
+        const int tt = t0 + lane + 64 * u;
+        v0[u] = tt < a.n_live ? e0[tt] : 0.0f;
+        v1[u] = tt < a.n_live ? e1[tt] : 0.0f;
       }
 #pragma unroll
-      for (int u = 0; u < 32; u++) acc = acc + v[u];
+      for (int u = 0; u < 32; u++) acc0 = acc0 + v0[u];
+#pragma unroll
+      for (int u = 0; u < 32; u++) acc1 = acc1 + v1[u];
     }
-    const float l = wave_sum(acc);  // the butterfly of the rule
-    if (lane == 0) inv[pr] = 1.0f / l;
+    const float l0 = wave_sum(acc0);  // the butterfly of the rule
+    const float l1 = wave_sum(acc1);
+    if (lane == 0) {
+      inv[pr] = 1.0f / l0;
+      if (two) inv[pr + 16] = 1.0f / l1;
+    }
   }
   __syncthreads();
-  const int t = blockIdx.x * 1024 + tid;
   if (t >= a.n_live) return;
   const bool re = a.placed && t == *a.placed;  // the slot evicted by this step
   const int sp = re ? a.posj : a.slot_pos[t];
   float acc = re ? 0.0f : a.attn_sum[t];
-  for (int i = 0; i < a.Sq; i++) {
+  if (sp <= a.qpos0) {
+#pragma unroll
+    for (int h = 0; h < NH; h++) acc = acc + ev0[h] * inv[h];
+  }
+  for (int i = 1; i < a.Sq; i++) {
     if (sp > a.qpos0 + i) continue;
     float ev[NH];
 #pragma unroll
