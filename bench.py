@@ -236,7 +236,8 @@ def main():
             arr[l].prep_cap = 0
         prep = {"us_per_token": round(prep_us, 2), "tokens": n,
                 "over_prepared_inputs_us": round(prep_us - us_tok, 2),
-                "kernels": "producers inside k_decode_attend / k_decode_finish"}
+                "kernels": "producers inside k_decode_attend (prepared rows stored for "
+                             "k_decode_finish)"}
         log(f"decode with fused QK producers: {prep_us:.2f} us/token "
             f"({prep_us - us_tok:+.2f} against prepared inputs)")
 
