@@ -1,7 +1,7 @@
 // decode.hip -- flash-decoding over the group-64 FP8 cache on gfx950
 // (engine.cu:386-480) and the entry points of the fused causal prefill
 // (engine.cu:236-308, kernel in prefill_mfma.hip) and of the matrix-core
-// decode (decode_mfma.hip).
+// decode (decode_kv.hip).
 //
 // The reference launches one block per (query head, split) and so reads
 // every K/V byte four times (once per query head of a GQA group).  Here a

@@ -1,0 +1,724 @@
+// decode_kv.hip -- flash-decoding of one query over the group-64 FP8 cache on
+// gfx950 matrix cores, in one launch (replaces the launch pair
+// attn_decode_split -> attn_decode_combine, engine.cu:386-480, with the
+// library's own split; the fresh token's tail write, engine.cu:190-198, and
+// the group commit on the step that fills the group, engine.cu:202-228,
+// ride along).
+//
+// Work split.  Workgroup = (kv head g, key range r); 8R workgroups, R ranges
+// per kv head (R = 1, or even and at most 32).  Workgroups go to the 8 XCDs
+// round-robin (XCD = blockIdx mod 8), and the numbering puts kv heads 2j and
+// 2j + 1 of the same range on one XCD: a kv head's 64 bytes are half of a
+// 128-byte line, and when the two halves are fetched by different XCDs
+// every line crosses the fabric twice (measured: a plain read of the same
+// bytes at half the rate).
+//
+// FP8 waves (8 per workgroup).  The committed groups of kv head g are
+// spread evenly over the 8R waves of the kv head (whole 64-key groups), and
+// a wave takes its groups two at a time (a unit: 8 KiB of K, 8 KiB of V).
+// A unit reaches the wave's LDS by DMA (global_load_lds_dwordx4, no staging registers): 16
+// keys x 64 bytes per instruction, lane i's 16 bytes at base + 16 i, blocks
+// of 16 keys padded to 1040 bytes.
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16 with the four k-groups of the
+//     operands holding four different key blocks (block-diagonal Q^T), so
+//     the 16 output columns are (key block b, query head i) and every
+//     column is real.  A = K: lane (c, r) holds key
+//     16 (r & 3) + (r >> 2) + 4c of the tile, 8 dims, read as 16 bytes per
+//     two products and converted fp8 -> fp16 exactly.  Output lane (c, n)
+//     with n = 4b + i holds keys 16v + 4b + c (v = 0..3) of head i.
+//   Online softmax in registers (scale and K group scale folded, log2
+//     units), reduced over the 16 lanes of a head.
+//   O = P V with P as the A operand as it stands: in product mu the
+//     k-group c of V holds key block (c + mu) & 3 and a lane's P is used
+//     only when its block is that one.  V comes from LDS through
+//     ds_read_b64_tr_b8 (8 keys of one dim per lane).  The V group scale is
+//     folded into P.  Output rows are (key block, head), summed over the
+//     blocks at the end.
+//   LDS reads of both operands are per-lane base + immediate and
+//   bank-conflict-free (K: 8 lanes of a b128 read hit 8 distinct 16-byte
+//   slots of a 128-byte bank cycle; V: the 16 lanes of a tr_b8 block hit 16
+//   distinct 8-byte slots).
+// Tail waves (4, only in the workgroup of range 0).  Wave i takes query head
+//   4g + i over the fp16 tail (keys committed..qpos): lane = key for the
+//   scores, lane = dim for P V.  With a fresh token it writes the token into
+//   the tail, and on the step whose token fills the group it quantises the
+//   group (bytes and scales bit-exact with kv_commit_group) and attends it
+//   in its FP8 form, as the reference does after its commit.
+// Merge.  Each workgroup merges its waves in LDS into one partial (m, l,
+//   o[64]) per query head.  With R > 1 it stores the partial with
+//   agent-coherent stores, waits until they have reached the agent, and
+//   takes a ticket from kv head g's arrival counter (one device-scope atomic
+//   per workgroup).  The workgroup that draws the last ticket resets the
+//   counter, fetches the R partials in one batch of coherent loads and
+//   writes the output.  Measured on this part, against this order:
+//   - epoch-tagged 64-bit partial words stored with no wait, polled by one
+//     merging workgroup (a word per writer, then the whole set) or by the
+//     first R/2 workgroups (a slice of outputs each): coherent loads of words
+//     whose stores are still in flight took 2-3 us, and the kernel lost
+//     1-2 us per layer against this order;
+//   - release / acquire fences at agent scope (buffer_wbl2 / buffer_inv): about
+//     10 us each;
+//   - a device-scope atomic round trip: about 0.25 us idle, 0.4-0.5 us under
+//     the stream; the acknowledgement of agent-coherent stores about 0.6 us.
+#include <type_traits>
+
+#include "attn_range.h"
+#include "qk_prep.h"
+
+namespace cia {
+
+constexpr int kFpWaves = 8;                // FP8 waves per workgroup
+constexpr int kTailWaves = GQA;            // tail waves (workgroup of range 0)
+constexpr int kDecThreads = 64 * (kFpWaves + kTailWaves);
+constexpr int kMaxRanges = 32;             // workgroups per kv head
+constexpr int kBlkB = 16 * 64 + 16;        // 16 keys x 64 B + 16 B pad
+constexpr int kTileB = 4 * kBlkB;          // one 64-key group of one kv head
+constexpr int kHalfB = 2 * kTileB;         // K (or V) of a unit
+constexpr int kScaleB = 256;               // K (or V) scales of a unit: 64 dwords, 2 used
+// LDS arena (one object: with several, the compiler tracks the LDS DMA
+// conservatively and turns the exact waits below into waits for everything)
+constexpr int kLdsK = 0;                                  // [8 waves][kHalfB]
+constexpr int kLdsV = kLdsK + kFpWaves * kHalfB;          // [8 waves][kHalfB]
+constexpr int kLdsScale = kLdsV + kFpWaves * kHalfB;      // [8 waves][2 slots][K, V][kScaleB]
+constexpr int kLdsQ = kLdsScale + kFpWaves * 4 * kScaleB; // fp16 q rows [4][64] + 128 zero bytes
+constexpr int kLdsKn = kLdsQ + (GQA * D + 64) * 2;        // fp16 fresh k row [64]
+constexpr int kLdsO = kLdsKn + D * 2;                     // f32 [9 partials][4][64]
+constexpr int kLdsML = kLdsO + (kFpWaves + 1) * GQA * D * 4;  // f32x2 [9][4]
+constexpr int kLdsTicket = kLdsML + (kFpWaves + 1) * GQA * 8;  // the workgroup's ticket
+constexpr int kLdsBytes = kLdsTicket + 16;
+constexpr int kPartRow = 4 + D;            // one head's partial: m, l, -, -, o[64]
+constexpr int kPartF = GQA * kPartRow;     // floats of one workgroup partial
+constexpr int kCntStride = 64;             // uint32 between the kv heads' counters (256 B)
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr int64_t kPartBytes = (int64_t)NKV * kMaxRanges * kPartF * sizeof(float);
+constexpr int64_t kWsBytes = kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+
+__device__ __forceinline__ f16x8 cvt8(uint32_t w0, uint32_t w1) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// max / sum over the 16 lanes of one head (lane bits 2..5; bits 0, 1 = head)
+__device__ __forceinline__ float head_max(float v) {
+  v = __builtin_fmaxf(v, row_ror<4>(v));
+  v = __builtin_fmaxf(v, row_ror<8>(v));
+  return col4_max(v);
+}
+__device__ __forceinline__ float head_sum(float v) {
+  v += row_ror<4>(v);
+  v += row_ror<8>(v);
+  return col4_sum(v);
+}
+
+// ds_read_b64_tr_b8 (within each 16-lane block, lane i receives byte i mod 8
+// of the 8-byte rows addressed by lanes 2k + (i div 8), k = 0..7), issued as
+// inline assembly: the compiler treats the builtin as touching every LDS
+// byte a pending DMA may write and would wait for all of them.  The result is
+// used only after lds_wait4.
+template <int kOff>
+__device__ __forceinline__ u32x2 ds_read_tr8_at(const uint8_t* p) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2"
+               : "=v"(v)
+               : "v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p), "i"(kOff));
+  return v;
+}
+#define ds_read_tr8(p, off) ds_read_tr8_at<off>(p)
+// waits for the LDS reads above and ties their results to the wait, so no
+// use is scheduled before it
+__device__ __forceinline__ void lds_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t nrec) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, nrec, 0x00020000);
+}
+constexpr int kCoherent = 16;  // sc1: agent-scope coherent access (L2 write-through / miss)
+
+struct DecArgs {
+  const uint16_t* q;     // [32][64], raw when prep.qw is set
+  uint8_t* kc8;          // written only when the fresh token completes a group
+  uint8_t* vc8;
+  uint16_t* ksc;
+  uint16_t* vsc;
+  uint16_t* ktail;
+  uint16_t* vtail;
+  const uint16_t* knew;  // fresh token [8][64] (key qpos, raw with prep), or null
+  const uint16_t* vnew;
+  int committed, qpos;
+  float scale;
+  float* part;           // [8][kMaxRanges][4][kPartRow] partials
+  uint32_t* cnt;         // [8] arrival counters, kCntStride apart; zero between calls
+  uint16_t* out;         // [32][64]
+  int ng;                // committed groups
+  int R;                 // workgroups per kv head
+  QkPrep prep;
+};
+
+// ---------------------------------------------------------------- kernel
+// grid = 8R, block = kDecThreads.  kPrep: q (and the fresh k) arrive raw and
+// the QK producers (engine.cu:799-801) run here.
+template <bool kPrep>
+__global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  uint16_t* sq = (uint16_t*)(lds + kLdsQ);
+  uint16_t* skn = (uint16_t*)(lds + kLdsKn);
+  float* sO = (float*)(lds + kLdsO);    // [p][i][d] at (p * 4 + i) * 64 + d
+  f32x2* sml = (f32x2*)(lds + kLdsML);  // [p][i] at p * 4 + i
+
+  const int bx = blockIdx.x, xcd = bx & 7, yy = bx >> 3;
+  int g, r;
+  if (a.R == 1) {
+    g = xcd;
+    r = 0;
+  } else {
+    g = 2 * (xcd & 3) + (yy & 1);
+    r = (xcd >> 2) * (a.R >> 1) + (yy >> 1);
+  }
+  const int tid = threadIdx.x, l = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (w >= kFpWaves && r != 0) return;  // tail waves live in range 0 only
+  const float qscale = a.scale * kLog2e;
+
+  // ================================================================ FP8 waves
+  if (w < kFpWaves) {
+    const int n = l & 15, c = l >> 4;  // MFMA column / k-group of this lane
+    const int om = r * kFpWaves + w, nwv = a.R * kFpWaves;
+    // this wave's committed groups [g0, g1), taken two at a time from g0 (a
+    // unit: groups s and s + 1; the second masked when s + 1 == g1)
+    const int g0 = (int)(((unsigned)om * (unsigned)a.ng) / (unsigned)nwv);
+    const int g1 = (int)(((unsigned)(om + 1) * (unsigned)a.ng) / (unsigned)nwv);
+    // (w & 7: the compiler then sees that a wave's DMA targets stay inside
+    // the tile and scale regions, and does not make reads of the q rows wait
+    // for them)
+    uint8_t* kw = lds + kLdsK + (w & 7) * kHalfB;
+    uint8_t* vw = lds + kLdsV + (w & 7) * kHalfB;
+    uint8_t* sw = lds + kLdsScale + (w & 7) * 4 * kScaleB;
+    // Waves 0-3 fetch the raw q row of head 4g + w (and the norm weights)
+    // by DMA into a staging area (the partial area, unused until the merge)
+    // ahead of their stream, and normalise / copy it into the q rows while
+    // the stream is in flight.  (Nothing loaded into registers is used after
+    // a wave's DMA has started: vmcnt counts in order, so such a use would
+    // wait for the whole unit.)
+    uint8_t* qstage = lds + kLdsO + (w & 3) * 1024;
+    if (w < GQA) {
+      // 8 lanes x 16 bytes; the resource covers just the row, so lanes 8..63
+      // read nothing (and write zeros into the rest of the staging slot)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.q + (size_t)(g * GQA + w) * D, 2 * D),
+                                               (lds_void_t*)qstage, 16, 16 * l, 0, 0, 0);
+      if constexpr (kPrep)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.prep.qw, 2 * D),
+                                                 (lds_void_t*)(qstage + 4096), 16, 16 * l, 0, 0, 0);
+    }
+    // A unit's data by DMA through buffer resources: each lane's VGPR
+    // operand is a fixed offset and the unit's position goes in the scalar
+    // offset (the compiler waits on a DMA before overwriting a VGPR the DMA
+    // used, so per-unit VGPR addresses would cost a full wait).  With no
+    // committed group the resources have no records: the fetch reads nothing.
+    const uint32_t nrec = a.ng > 0 ? 0x7fffffffu : 0u;
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.kc8, nrec), rv = buf_rsrc(a.vc8, nrec);
+    //   (the scale resources end at the last committed group)
+    const uint32_t nsc = (uint32_t)a.ng * (NKV * 2);
+    const __amdgpu_buffer_rsrc_t rks = buf_rsrc(a.ksc, nsc), rvs = buf_rsrc(a.vsc, nsc);
+    //   K or V: lane l fetches key (l >> 2) of a 16-key block, chunk l & 3
+    const uint32_t loff = (uint32_t)((l >> 2) * (NKV * D) + g * D + 16 * (l & 3));
+    //   group scales of kv head g, groups s - sh (even lanes) and s - sh + 1
+    //   (odd lanes): dwords 0, 1 of the slot (K) and of slot + 256 (V).  sh = 1
+    //   when s is the last committed group (s + 1 has no scale), so group s
+    //   is in dword sh.
+    const uint32_t soff = (uint32_t)(((l & 1) * NKV + g) * 2);
+    auto scale_shift = [&](int u) { return u + 1 >= a.ng && u > 0 ? 1 : 0; };
+    auto issue_scales = [&](int u, uint8_t* slot) {
+      const uint32_t so = (uint32_t)(u - scale_shift(u)) * (NKV * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rks, (lds_void_t*)slot, 2, soff, so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (lds_void_t*)(slot + kScaleB), 2, soff, so, 0, 0);
+    };
+    auto issue = [&](int u, __amdgpu_buffer_rsrc_t rc, uint8_t* dst) {
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int grp = u + t < g1 ? u + t : u;  // past the range: refetch
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rc, (lds_void_t*)(dst + t * kTileB + j * kBlkB), 16, loff,
+              (uint32_t)grp * (G * NKV * D) + (uint32_t)j * (16 * NKV * D), 0, 0);
+      }
+    };
+    // (a wave without units fetches unit 0 and ignores it)
+    const int uf = g0 < g1 ? g0 : 0;
+    // Each wave fetches a unit's V only once the unit's K has landed (its K
+    // DMAs then hold no more slots, so the V DMAs rarely wait to issue), and
+    // multiplies K while V streams in: the workgroup's K lands first and
+    // only P V follows the last bytes.
+    __builtin_amdgcn_sched_barrier(0);
+    issue_scales(uf, sw);
+    issue(uf, rk, kw);
+    __builtin_amdgcn_sched_barrier(0);
+    if (w < GQA) {
+      // the q row landed once at most the unit's 10 scale and K DMAs remain
+      __builtin_amdgcn_s_waitcnt(0x0F7A);  // vmcnt(10)
+      const uint16_t raw = ((const uint16_t*)qstage)[l];
+      if constexpr (kPrep) {
+        // RoPE frequency of lane l (the table is in the kernel arguments,
+        // read as scalars and selected per lane)
+        // (readfirstlane keeps the compiler from turning the selects back
+        // into a per-lane load)
+        float invf = 0.f;
+#pragma unroll
+        for (int k = 0; k < D / 2; k++) {
+          const float fk = __builtin_bit_cast(
+              float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a.prep.rt.invf[k])));
+          invf = (l & 31) == k ? fk : invf;
+        }
+        float sn, cs;
+        rope_sincos_f(invf, a.qpos, sn, cs);
+        const uint16_t wq = ((const uint16_t*)(qstage + 4096))[l];
+        sq[w * D + l] = qk_norm_rope_sc(h2f(raw), h2f(wq), l, sn, cs, a.prep.eps);
+      } else {
+        sq[w * D + l] = raw;
+      }
+      if (w == 0) sq[GQA * D + l] = 0;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS stores done (DMA still in flight)
+    __builtin_amdgcn_s_barrier();        // B1: q rows in LDS
+    // B operand of S^T: lane (c, n = 4b + i) holds head i's dims when b == c
+    f16x8 qop[8];
+    {
+      const int qoff = ((n >> 2) == c ? (n & 3) * D : GQA * D) * 2;
+#pragma unroll
+      for (int m = 0; m < 8; m++)
+        qop[m] = *(const f16x8*)((const uint8_t*)sq + qoff + 16 * m);
+    }
+    // per-lane LDS offsets: K reads (key 16 (n & 3) + (n >> 2) + 4c), V
+    // transposed reads (lane 2k + h of a 16-lane block: key
+    // 64 (k >> 2) + 16 (k & 3) + 4 beta + c, dims 8h..8h+7 of the chunk)
+    const int krd = (n & 3) * kBlkB + 64 * ((n >> 2) + 4 * c);
+    int vrd[4];
+    {
+      const int k = n >> 1, h = n & 1;
+      const int base = (k >> 2) * kTileB + (k & 3) * kBlkB + 64 * c + 8 * h;
+#pragma unroll
+      for (int mu = 0; mu < 4; mu++) vrd[mu] = base + 256 * ((c + mu) & 3);
+    }
+    float mx = -1e30f, lsum = 0.f;  // head n & 3, replicated over its 16 lanes
+    f32x4 O[4];                     // [dims 16 delta + n][rows (block c, head v)]
+#pragma unroll
+    for (int d = 0; d < 4; d++) O[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f16x2 one2 = f16x2{(_Float16)1.0f, (_Float16)1.0f};
+    // One unit (slot = which scale slot holds its scales): wait for its
+    // scales and K, fetch its V, S^T, then (kMore) the next unit's scales and
+    // K once this unit's K is read; softmax; wait for V; P V.  No load sits
+    // under a branch, so every wait is exact.
+    auto unit = [&](int u, int slot, auto more_tag) {
+      constexpr bool kMore = decltype(more_tag)::value;
+      const bool t1ok = u + 1 < g1;
+      // ---- S^T = K Q^T once the scales and K landed; V goes out now
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
+      issue(u, rv, vw);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t* scl = (const uint32_t*)(sw + slot * 2 * kScaleB);
+      const int sh = scale_shift(u);  // (then group u + 1 is masked)
+      const float ks0 = h2f((uint16_t)scl[sh]) * qscale, ks1 = h2f((uint16_t)scl[1]) * qscale;
+      const _Float16 vs0 = __builtin_bit_cast(_Float16, (uint16_t)scl[kScaleB / 4 + sh]);
+      const _Float16 vs1 = __builtin_bit_cast(_Float16, (uint16_t)scl[kScaleB / 4 + 1]);
+      f32x4 S[2];
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m2 = 0; m2 < 4; m2++) {
+          const u32x4 kk = *(const u32x4*)(kw + krd + t * kTileB + 16 * m2);
+          S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[0], kk[1]), qop[2 * m2], S[t], 0, 0, 0);
+          S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[2], kk[3]), qop[2 * m2 + 1], S[t], 0, 0, 0);
+        }
+      }
+      if constexpr (kMore) {
+        // this unit's K (and the other scale slot) fully read: the next
+        // unit's may overwrite them
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_scales(u + 2, sw + (slot ^ 1) * 2 * kScaleB);
+        issue(u + 2, rk, kw);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // ---- online softmax over the unit's 128 keys (4 per lane and tile)
+      float rmx = -1e30f;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          S[t][v] *= t ? ks1 : ks0;
+          if (t == 1 && !t1ok) S[t][v] = -1e30f;
+          rmx = __builtin_fmaxf(rmx, S[t][v]);
+        }
+      rmx = head_max(rmx);
+      const float mnew = __builtin_fmaxf(mx, rmx);
+      const float corr = __builtin_amdgcn_exp2f(mx - mnew);
+      mx = mnew;
+      f16x8 P;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) P[4 * t + v] = (_Float16)__builtin_amdgcn_exp2f(S[t][v] - mnew);
+      float rs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) rs = __builtin_amdgcn_fdot2(f16x2{P[2 * e], P[2 * e + 1]}, one2, rs, false);
+      rs = head_sum(rs);
+      lsum = __builtin_fmaf(lsum, corr, rs);
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        P[v] *= vs0;
+        P[4 + v] *= vs1;
+      }
+      // corrections of the four heads (lanes 0..3 are heads 0..3)
+      float oc[4];
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        oc[v] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), v));
+      // ---- O = O corr + (P sv) V
+      if constexpr (kMore) __builtin_amdgcn_s_waitcnt(0x0F7A);  // vmcnt(10): next scales + K in flight
+      else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+      const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      f32x4 T[4];
+#pragma unroll
+      for (int d = 0; d < 4; d++) T[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mu = 0; mu < 4; mu++) {
+        const f16x8 A = ((n >> 2) == ((c + mu) & 3)) ? P : zero8;
+        u32x2 raw0 = ds_read_tr8(vw + vrd[mu], 0), raw1 = ds_read_tr8(vw + vrd[mu], 16);
+        u32x2 raw2 = ds_read_tr8(vw + vrd[mu], 32), raw3 = ds_read_tr8(vw + vrd[mu], 48);
+        lds_wait4(raw0, raw1, raw2, raw3);
+        T[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw0[0], raw0[1]), T[0], 0, 0, 0);
+        T[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw1[0], raw1[1]), T[1], 0, 0, 0);
+        T[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw2[0], raw2[1]), T[2], 0, 0, 0);
+        T[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw3[0], raw3[1]), T[3], 0, 0, 0);
+      }
+      if constexpr (kMore) {
+        // this unit's V fully read before the next unit's V overwrites it
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+      }
+#pragma unroll
+      for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) O[d][v] = __builtin_fmaf(O[d][v], oc[v], T[d][v]);
+    };
+    int slot = 0;
+    int u = g0;
+    for (; u + 2 < g1; u += 2, slot ^= 1) unit(u, slot, std::integral_constant<bool, true>{});
+    if (u < g1) unit(u, slot, std::integral_constant<bool, false>{});
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // (a wave without units: its fetch done)
+    // ---- the four key blocks of each (head, dim) summed; lanes 0..15 hold
+    // O[head v][16 delta + n]
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) O[d][v] = col4_sum(O[d][v]);
+    if (l < 16) {
+#pragma unroll
+      for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = O[d][v];
+    }
+    if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
+  } else {
+    // ============================================================ tail waves
+    const int i = w - kFpWaves;  // query head 4g + i
+    const int tt = a.qpos + 1 - a.committed;  // tail keys (the fresh token last)
+    const bool fresh = a.knew != nullptr;
+    const bool commit = fresh && tt == G;
+    if (fresh && i == 0) {
+      // the fresh token: k prepared when raw, kept in LDS for the scores and
+      // written into its tail row with v (engine.cu:190-198)
+      const uint16_t kraw = a.knew[g * D + l];
+      uint16_t kv;
+      if constexpr (kPrep)
+        kv = qk_norm_rope_lane(h2f(kraw), h2f(a.prep.kw[l]), l, a.qpos, a.prep.eps, a.prep.rt);
+      else
+        kv = kraw;
+      skn[l] = kv;
+      a.ktail[((size_t)(tt - 1) * NKV + g) * D + l] = kv;
+      a.vtail[((size_t)(tt - 1) * NKV + g) * D + l] = a.vnew[g * D + l];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();  // B1: q rows and the fresh k in LDS
+    // ---- scores: lane = key
+    const bool live = l < tt;
+    const int krow = live ? l : 0;  // (tail row 0 exists whatever the tail length)
+    const uint16_t* kp = a.ktail + ((size_t)krow * NKV + g) * D;
+    u32x4 kq[8], qq[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(kp + 8 * cc);
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) qq[cc] = *(const u32x4*)(sq + i * D + 8 * cc);
+    if (fresh && l == tt - 1) {
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(skn + 8 * cc);
+    }
+    float x;
+    if (!commit) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) {
+        const f16x8 q8 = __builtin_bit_cast(f16x8, qq[cc]), k8 = __builtin_bit_cast(f16x8, kq[cc]);
+        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 0, 1), __builtin_shufflevector(k8, k8, 0, 1), sacc, false);
+        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 2, 3), __builtin_shufflevector(k8, k8, 2, 3), sacc, false);
+        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 4, 5), __builtin_shufflevector(k8, k8, 4, 5), sacc, false);
+        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 6, 7), __builtin_shufflevector(k8, k8, 6, 7), sacc, false);
+      }
+      x = sacc * qscale;
+    } else {
+      // The fresh token fills the group: kv_commit_group (engine.cu:202-228)
+      // of kv head g, and the group is attended in its FP8 form.  Lane l
+      // quantises key l; wave 0 writes the bytes and the scale.
+      float kf[D];
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          kf[8 * cc + 2 * e] = h2f((uint16_t)kq[cc][e]);
+          kf[8 * cc + 2 * e + 1] = h2f((uint16_t)(kq[cc][e] >> 16));
+        }
+      float ak = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; d++) ak = __builtin_fmaxf(ak, __builtin_fabsf(kf[d]));
+      const float sck = quant_scale(wave_max_fast(ak));
+      const uint16_t skh = f2h(sck);
+      const float kdq = h2f(skh);
+      uint8_t* krow8 = a.kc8 + ((size_t)(a.committed + l) * NKV + g) * D;
+      float sacc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const uint32_t kb = e4m3x4(kf[4 * j] / sck, kf[4 * j + 1] / sck, kf[4 * j + 2] / sck,
+                                   kf[4 * j + 3] / sck);
+        const f16x8 q8 = __builtin_bit_cast(f16x8, qq[j >> 1]);
+        const int o4 = (j & 1) * 4;
+        sacc = __builtin_fmaf((float)q8[o4 + 0], e4m3_to_f32<0>(kb) * kdq, sacc);
+        sacc = __builtin_fmaf((float)q8[o4 + 1], e4m3_to_f32<1>(kb) * kdq, sacc);
+        sacc = __builtin_fmaf((float)q8[o4 + 2], e4m3_to_f32<2>(kb) * kdq, sacc);
+        sacc = __builtin_fmaf((float)q8[o4 + 3], e4m3_to_f32<3>(kb) * kdq, sacc);
+        if (i == 0) *(uint32_t*)(krow8 + 4 * j) = kb;
+      }
+      if (i == 0 && l == 0) a.ksc[(a.committed / G) * NKV + g] = skh;
+      x = sacc * qscale;
+    }
+    x = live ? x : -1e30f;
+    const float M = wave_max_fast(x);
+    const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
+    const float L = wave_sum_fast(p);
+    // ---- P V: lane = dim; V rows of the tail (the fresh row from vnew)
+    float o = 0.f;
+    if (!commit) {
+      for (int k0 = 0; k0 < tt; k0 += 16) {
+        float vv[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int k = k0 + e < tt ? k0 + e : 0;
+          const uint16_t* vp = (fresh && k == tt - 1) ? a.vnew + g * D : a.vtail + ((size_t)k * NKV + g) * D;
+          vv[e] = h2f(vp[l]);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k0 + e));
+          if (k0 + e < tt) o = __builtin_fmaf(pk, vv[e], o);
+        }
+      }
+    } else {
+      // the whole group (tt == 64): V quantised with its group scale
+      float vv[G];
+#pragma unroll
+      for (int k = 0; k < G; k++) {
+        const uint16_t* vp = k == G - 1 ? a.vnew + g * D : a.vtail + ((size_t)k * NKV + g) * D;
+        vv[k] = h2f(vp[l]);
+      }
+      float av = 0.f;
+#pragma unroll
+      for (int k = 0; k < G; k++) av = __builtin_fmaxf(av, __builtin_fabsf(vv[k]));
+      const float scv = quant_scale(wave_max_fast(av));
+      const uint16_t svh = f2h(scv);
+      const float vdq = h2f(svh);
+#pragma unroll
+      for (int k = 0; k < G; k++) {
+        const uint32_t vb = e4m3x2(vv[k] / scv, 0.f) & 0xFFu;
+        if (i == 0) a.vc8[((size_t)(a.committed + k) * NKV + g) * D + l] = (uint8_t)vb;
+        const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
+        o = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, o);
+      }
+      if (i == 0 && l == 0) a.vsc[(a.committed / G) * NKV + g] = svh;
+    }
+    sO[(kFpWaves * GQA + i) * D + l] = o;
+    if (l == 0) sml[kFpWaves * GQA + i] = f32x2{M, L};
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // B2: every wave's partial in LDS
+
+  // ================================================================ merge
+  if (w >= kFpWaves) return;  // (tail waves: their partial is in LDS)
+  const int R = a.R;
+  float* pg = a.part + (size_t)g * kMaxRanges * kPartF;  // kv head g's partials
+  if (tid < GQA * D) {
+    // the workgroup's partial of (head 4g + i, dim d)
+    const int i = tid >> 6, d = tid & 63;
+    const int np = r == 0 ? kFpWaves + 1 : kFpWaves;
+    // (every read first, then the arithmetic: the reads go out together)
+    f32x2 ml[kFpWaves + 1];
+    float ov[kFpWaves + 1];
+#pragma unroll
+    for (int p = 0; p <= kFpWaves; p++) {
+      const int pp = p < np ? p : 0;
+      ml[p] = sml[pp * GQA + i];
+      ov[p] = sO[(pp * GQA + i) * D + d];
+    }
+    float M = -1e30f;
+#pragma unroll
+    for (int p = 0; p <= kFpWaves; p++) M = p < np ? __builtin_fmaxf(M, ml[p][0]) : M;
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int p = 0; p <= kFpWaves; p++) {
+      const float wt = p < np ? __builtin_amdgcn_exp2f(ml[p][0] - M) : 0.f;
+      L = __builtin_fmaf(ml[p][1], wt, L);
+      O = __builtin_fmaf(ov[p], wt, O);
+    }
+    if (R == 1) {
+      a.out[(size_t)(g * GQA + i) * D + d] = f2h(O * (1.0f / L));
+    } else {
+      float* row = pg + (size_t)(r * GQA + i) * kPartRow;
+      __hip_atomic_store(row + 4 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have reached the agent
+    }
+  }
+  if (R == 1) return;
+  __builtin_amdgcn_s_barrier();  // B3: the workgroup's partial stored
+  uint32_t* ctr = a.cnt + g * kCntStride;
+  uint32_t* sticket = (uint32_t*)(lds + kLdsTicket);
+  if (tid == 0) *sticket = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // B4
+  if (*sticket != (uint32_t)(R - 1)) return;
+  // ---- the last workgroup of kv head g to arrive: every partial stored.
+  // The counter goes back to zero for the next call.
+  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float* sp = (float*)(lds + kLdsK);  // [R][4][kPartRow] (the K tiles are free)
+  {
+    // the R partials, 16 bytes per load, one batch per thread
+    constexpr int kPer = (kMaxRanges * kPartF / 4 + 64 * kFpWaves - 1) / (64 * kFpWaves);
+    const int nvec = R * (kPartF / 4);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(pg);
+    u32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int e = tid + 64 * kFpWaves * k;
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (e < nvec ? e : 0) * 16, 0, kCoherent);
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int e = tid + 64 * kFpWaves * k;
+      if (e < nvec) *(u32x4*)(sp + 4 * e) = v[k];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();  // B5
+  if (tid < GQA * D) {
+    // wave i = query head 4g + i: lane p weighs partial p, then lane d sums
+    // dim d (the row reads go out together; the weights come from lane p)
+    const int i = w, lane = l;
+    const f32x2 mlp = *(const f32x2*)(sp + (size_t)((lane < R ? lane : 0) * GQA + i) * kPartRow);
+    float ov[kMaxRanges];
+#pragma unroll
+    for (int p = 0; p < kMaxRanges; p++) ov[p] = sp[((p < R ? p : 0) * GQA + i) * kPartRow + 4 + lane];
+    const bool ok = lane < R && mlp[1] > 0.f;
+    const float M = wave_max_fast(ok ? mlp[0] : -1e30f);
+    const float wt = ok ? __builtin_amdgcn_exp2f(mlp[0] - M) : 0.f;
+    const float L = wave_sum_fast(ok ? mlp[1] * wt : 0.f);
+    float O = 0.f;
+#pragma unroll
+    for (int p = 0; p < kMaxRanges; p++)
+      O = __builtin_fmaf(ov[p], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), p)), O);
+    a.out[(size_t)(g * GQA + i) * D + lane] = f2h(O * (1.0f / L));
+  }
+}
+
+}  // namespace cia
+
+using namespace cia;
+
+// compute units of the current device (0 if unknown)
+static int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// workgroups per kv head: about two groups per FP8 wave, 1 or even, <= 32,
+// and at most one workgroup per compute unit over the 8 kv heads (a
+// workgroup fills a CU's LDS; the cap keeps the whole grid resident at once)
+static int dec_ranges(int ng) {
+  int R = (ng + 2 * kFpWaves - 1) / (2 * kFpWaves);
+  if (R <= 1) return 1;
+  R += R & 1;
+  int cap = kMaxRanges;
+  const int cus = device_cus();
+  if (cus > 0 && cus / NKV < cap) cap = (cus / NKV) & ~1;
+  if (cap < 2) return 1;
+  return R > cap ? cap : R;
+}
+
+extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
+  return max_tokens < 0 ? 0 : kWsBytes;
+}
+
+// Flash-decoding with the library's split and, when knew/vnew are given, the
+// fresh token's tail write (and the group commit on the step it fills the
+// group) fused in.  Internal entry shared by cia_attn_decode and the layer
+// driver; mid_event (may be NULL) is recorded after the launch.  prep (may
+// be NULL): a QkPrep when q and knew arrive raw.
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, uint16_t* ktail, uint16_t* vtail, const uint16_t* knew,
+    const uint16_t* vnew, int committed, int qpos, float scale, uint16_t* out, void* ws,
+    int64_t ws_bytes, void* stream, void* mid_event, const void* prep) {
+  if (ws_bytes < kWsBytes) return CIA_ERR_ARG;
+  if (committed % G || committed > qpos + 1 || qpos + 1 - committed > G) return CIA_ERR_STATE;
+  if (knew && (!vnew || qpos + 1 - committed < 1)) return CIA_ERR_ARG;
+  const int ng = committed / G, R = dec_ranges(ng);
+  DecArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail,
+             knew, vnew, committed, qpos, scale, (float*)ws,
+             (uint32_t*)((char*)ws + kPartBytes), out, ng, R, QkPrep{}};
+  if (prep) da.prep = *(const QkPrep*)prep;
+  hipStream_t s = (hipStream_t)stream;
+  if (da.prep.qw)
+    hipLaunchKernelGGL(k_decode<true>, dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+  else
+    hipLaunchKernelGGL(k_decode<false>, dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+  int st = launch_status();
+  if (st) return st;
+  if (mid_event) {
+    const hipError_t e = hipEventRecord((hipEvent_t)mid_event, s);
+    if (e != hipSuccess) {
+      set_hip_error(e);
+      return CIA_ERR_HIP;
+    }
+  }
+  return CIA_OK;
+}

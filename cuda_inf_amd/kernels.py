@@ -120,14 +120,16 @@ def decode_workspace_bytes(max_tokens: int) -> int:
 
 
 def new_decode_workspace(max_tokens: int, device="cuda") -> torch.Tensor:
-    """Scratch of attn_decode (partial softmax states; no state between calls)."""
+    """Workspace of attn_decode: partial softmax states and per-kv-head
+    arrival counters.  Zeroed here; every call leaves the counters at zero."""
     return torch.zeros(decode_workspace_bytes(max_tokens), dtype=torch.uint8, device=device)
 
 
 def attn_decode(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int, scale: float,
                 out, ws) -> None:
-    """Flash-decoding on the matrix cores with the library's own split
-    (replaces engine.cu:848-852's split + combine launches)."""
+    """Flash-decoding on the matrix cores with the library's own split, one
+    launch (replaces engine.cu:848-852's split + combine launches).  Calls
+    sharing ws must be ordered on one stream."""
     call("cia_attn_decode", _dev(q, "q", _F16, NH * D),
          _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
          _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),

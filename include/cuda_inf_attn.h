@@ -147,19 +147,21 @@ int cia_attn_decode_combine(const float* pm, const float* pl, const float* po,
 
 /* Flash-decoding with the library's own split on the matrix cores (no
  * counterpart kernel in the reference; it replaces the pair of launches at
- * engine.cu:848-852 and computes the same attention).  One workgroup per
- * four 64-key FP8 groups of four kv heads, plus tail workgroups, then one
- * merge launch.  Requires committed <= qpos + 1 (the tail holds keys
- * committed..qpos).  ws: device scratch of at least
- * cia_decode_workspace_bytes(qpos + 1) bytes, passed with its size. */
+ * engine.cu:848-852 and computes the same attention) in ONE launch: up to
+ * 32 workgroups per kv head stream the FP8 groups, the first also takes the
+ * fp16 tail, and the last workgroup of each kv head to finish merges the
+ * partials.  Requires committed <= qpos + 1 (the tail holds keys
+ * committed..qpos).  ws: device memory of at least
+ * cia_decode_workspace_bytes(qpos + 1) bytes, passed with its size, ZEROED
+ * before its first use (it holds per-kv-head arrival counters, which every
+ * call leaves at zero again).  Calls that share a ws must not overlap. */
 int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                     const uint16_t* ksc, const uint16_t* vsc,
                     const uint16_t* ktail, const uint16_t* vtail,
                     int committed, int qpos, float scale, uint16_t* out,
                     void* ws, int64_t ws_bytes, void* stream);
-/* scratch bytes cia_attn_decode needs for contexts of up to max_tokens
- * (the same buffer as a layer's ws_decode also holds the prepared q and
- * fresh k rows, 5 KiB, of a decode step that runs the QK producers) */
+/* workspace bytes cia_attn_decode needs for contexts of up to max_tokens
+ * (also the size of a layer's ws_decode) */
 int64_t cia_decode_workspace_bytes(int max_tokens);
 
 /* ------------------------------------------------------------------ */
@@ -318,7 +320,8 @@ typedef struct cia_layer {
   /* flash-decoding */
   int nsplit;            /* 0 -> cia_attn_decode path with ws_decode */
   float* pm; float* pl; float* po;
-  void* ws_decode;       /* cia_decode_workspace_bytes(maxT) bytes */
+  void* ws_decode;       /* cia_decode_workspace_bytes(maxT) bytes, zeroed
+                            before first use */
   /* H2O (budget > 0 enables it) */
   int budget, window;
   uint8_t* kf; uint8_t* vf; uint16_t* ks; uint16_t* vs;
