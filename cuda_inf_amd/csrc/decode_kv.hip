@@ -60,6 +60,7 @@
 //     10 us each;
 //   - a device-scope atomic round trip: about 0.25 us idle, 0.4-0.5 us under
 //     the stream; the acknowledgement of agent-coherent stores about 0.6 us.
+#include <algorithm>
 #include <type_traits>
 
 #include "attn_range.h"
@@ -85,7 +86,11 @@ constexpr int kLdsKn = kLdsQ + (GQA * D + 64) * 2;        // fp16 fresh k row [6
 constexpr int kLdsO = kLdsKn + D * 2;                     // f32 [9 partials][4][64]
 constexpr int kLdsML = kLdsO + (kFpWaves + 1) * GQA * D * 4;  // f32x2 [9][4]
 constexpr int kLdsTicket = kLdsML + (kFpWaves + 1) * GQA * 8;  // the workgroup's ticket
-constexpr int kLdsBytes = kLdsTicket + 16;
+// the extra wave's one group: K tile, V tile, then its K and V scales
+constexpr int kLdsX = (kLdsTicket + 16 + 127) / 128 * 128;
+constexpr int kLdsXS = kLdsX + 2 * kTileB;
+constexpr int kLdsBytes = kLdsXS + 2 * kScaleB;
+static_assert(kLdsBytes <= 160 * 1024, "LDS");
 constexpr int kPartRow = 4 + D;            // one head's partial: m, l, -, -, o[64]
 constexpr int kPartF = GQA * kPartRow;     // floats of one workgroup partial
 constexpr int kCntStride = 64;             // uint32 between the kv heads' counters (256 B)
@@ -163,6 +168,8 @@ struct DecArgs {
   uint16_t* out;         // [32][64]
   int ng;                // committed groups
   int R;                 // workgroups per kv head
+  int ne;                // extra groups: the last ne groups, one each to wave 8
+                         // of workgroups 1..ne
   QkPrep prep;
 };
 
@@ -188,23 +195,36 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   }
   const int tid = threadIdx.x, l = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (w >= kFpWaves && r != 0) return;  // tail waves live in range 0 only
+  // Wave 8: a tail wave in range 0; in ranges 1..ne the extra wave, which
+  // takes one group (an FP8 wave with a one-group buffer in the LDS the
+  // others leave free).  The rest return.
+  const bool xw = w == kFpWaves && r != 0 && r <= a.ne;
+  if (w >= kFpWaves && r != 0 && !xw) return;
   const float qscale = a.scale * kLog2e;
 
   // ================================================================ FP8 waves
-  if (w < kFpWaves) {
+  if (w < kFpWaves || xw) {
     const int n = l & 15, c = l >> 4;  // MFMA column / k-group of this lane
-    const int om = r * kFpWaves + w, nwv = a.R * kFpWaves;
+    const int om = r * kFpWaves + w, nwv = a.R * kFpWaves, ngm = a.ng - a.ne;
     // this wave's committed groups [g0, g1), taken two at a time from g0 (a
-    // unit: groups s and s + 1; the second masked when s + 1 == g1)
-    const int g0 = (int)(((unsigned)om * (unsigned)a.ng) / (unsigned)nwv);
-    const int g1 = (int)(((unsigned)(om + 1) * (unsigned)a.ng) / (unsigned)nwv);
+    // unit: groups s and s + 1; the second masked when s + 1 == g1); the
+    // extra wave's: group ngm + r - 1
+    int g0, g1;
+    if (xw) {
+      g0 = ngm + r - 1;
+      g1 = g0 + 1;
+    } else {
+      g0 = (int)(((unsigned)om * (unsigned)ngm) / (unsigned)nwv);
+      g1 = (int)(((unsigned)(om + 1) * (unsigned)ngm) / (unsigned)nwv);
+    }
     // (w & 7: the compiler then sees that a wave's DMA targets stay inside
     // the tile and scale regions, and does not make reads of the q rows wait
-    // for them)
-    uint8_t* kw = lds + kLdsK + (w & 7) * kHalfB;
-    uint8_t* vw = lds + kLdsV + (w & 7) * kHalfB;
-    uint8_t* sw = lds + kLdsScale + (w & 7) * 4 * kScaleB;
+    // for them.)  The extra wave has one tile each of K and V: its second
+    // tile (always masked) is read from the first (tile stride ts = 0).
+    uint8_t* kw = xw ? lds + kLdsX : lds + kLdsK + (w & 7) * kHalfB;
+    uint8_t* vw = xw ? lds + kLdsX + kTileB : lds + kLdsV + (w & 7) * kHalfB;
+    uint8_t* sw = xw ? lds + kLdsXS : lds + kLdsScale + (w & 7) * 4 * kScaleB;
+    const int ts = xw ? 0 : kTileB;
     // Waves 0-3 fetch the raw q row of head 4g + w (and the norm weights)
     // by DMA into a staging area (the partial area, unused until the merge)
     // ahead of their stream, and normalise / copy it into the q rows while
@@ -247,6 +267,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     auto issue = [&](int u, __amdgpu_buffer_rsrc_t rc, uint8_t* dst) {
 #pragma unroll
       for (int t = 0; t < 2; t++) {
+        if (t == 1 && xw) break;  // (its one group)
         const int grp = u + t < g1 ? u + t : u;  // past the range: refetch
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -264,6 +285,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     issue_scales(uf, sw);
     issue(uf, rk, kw);
+    if (xw) issue(uf, rv, vw);  // (its one group: K and V at once)
     __builtin_amdgcn_sched_barrier(0);
     if (w < GQA) {
       // the q row landed once at most the unit's 10 scale and K DMAs remain
@@ -307,7 +329,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     int vrd[4];
     {
       const int k = n >> 1, h = n & 1;
-      const int base = (k >> 2) * kTileB + (k & 3) * kBlkB + 64 * c + 8 * h;
+      const int base = (k >> 2) * ts + (k & 3) * kBlkB + 64 * c + 8 * h;
 #pragma unroll
       for (int mu = 0; mu < 4; mu++) vrd[mu] = base + 256 * ((c + mu) & 3);
     }
@@ -326,7 +348,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       // ---- S^T = K Q^T once the scales and K landed; V goes out now
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       __builtin_amdgcn_sched_barrier(0);
-      issue(u, rv, vw);
+      if (!xw) issue(u, rv, vw);
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t* scl = (const uint32_t*)(sw + slot * 2 * kScaleB);
       const int sh = scale_shift(u);  // (then group u + 1 is masked)
@@ -339,7 +361,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m2 = 0; m2 < 4; m2++) {
-          const u32x4 kk = *(const u32x4*)(kw + krd + t * kTileB + 16 * m2);
+          const u32x4 kk = *(const u32x4*)(kw + krd + t * ts + 16 * m2);
           S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[0], kk[1]), qop[2 * m2], S[t], 0, 0, 0);
           S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cvt8(kk[2], kk[3]), qop[2 * m2 + 1], S[t], 0, 0, 0);
         }
@@ -570,7 +592,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   if (tid < GQA * D) {
     // the workgroup's partial of (head 4g + i, dim d)
     const int i = tid >> 6, d = tid & 63;
-    const int np = r == 0 ? kFpWaves + 1 : kFpWaves;
+    const int np = r == 0 || r <= a.ne ? kFpWaves + 1 : kFpWaves;
     // (every read first, then the arithmetic: the reads go out together)
     f32x2 ml[kFpWaves + 1];
     float ov[kFpWaves + 1];
@@ -702,9 +724,11 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   if (committed % G || committed > qpos + 1 || qpos + 1 - committed > G) return CIA_ERR_STATE;
   if (knew && (!vnew || qpos + 1 - committed < 1)) return CIA_ERR_ARG;
   const int ng = committed / G, R = dec_ranges(ng);
+  // groups past 16 per workgroup go one each to the extra waves
+  const int ne = R > 1 ? std::min(std::max(ng - 16 * R, 0), R - 1) : 0;
   DecArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail,
              knew, vnew, committed, qpos, scale, (float*)ws,
-             (uint32_t*)((char*)ws + kPartBytes), out, ng, R, QkPrep{}};
+             (uint32_t*)((char*)ws + kPartBytes), out, ng, R, ne, QkPrep{}};
   if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
   if (da.prep.qw)
