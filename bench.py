@@ -28,19 +28,13 @@ import time
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8
+TRAFFIC_FILE = "profiles/decode_ctx32k_traffic.json"
 
 
 def algo_bytes(Tc: int, Tt: int) -> int:
     """Algorithmic bytes of one layer's decode: FP8 K+V, fp16 group scales,
     fp16 tail K+V, q in and out."""
     return 1024 * Tc + (Tc // 64) * 8 * 2 * 2 + 2048 * Tt + 8192
-
-
-def attend_bytes(Tc: int) -> int:
-    """Algorithmic bytes of the attend launch alone: the committed FP8 K+V,
-    their fp16 group scales and q (the tail and the output belong to the
-    finish launch)."""
-    return 1024 * Tc + (Tc // 64) * 8 * 2 * 2 + 4096
 
 
 def main():
@@ -51,14 +45,14 @@ def main():
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=6)
     ap.add_argument("--nsplit", type=int, default=0,
-                    help="0: matrix-core decode (attend + finish launches); "
+                    help="0: matrix-core decode (one launch per layer); "
                          ">0: the reference's split+combine with this split count")
     ap.add_argument("--cold-steps", type=int, default=32)
     ap.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", type=float, default=None,
-                    help="HBM bytes per attend launch measured with rocprofv3 --pmc "
+                    help="HBM bytes per decode launch measured with rocprofv3 --pmc "
                          "(FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), reported as "
                          "roofline.traffic")
     ap.add_argument("--long-ctx", type=int, default=131072,
@@ -162,33 +156,54 @@ def main():
     timed_bytes = bytes_of_steps(s_timed, K)
     log(f"warm: {us_tok:.2f} us/token, effective {timed_bytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s")
 
-    # The decode launch pair (k_decode_attend + k_decode_finish) is the
-    # dominant work: its average duration is the timed region's span over
-    # its K * layers launches (events bracket the region on the kernels' own
-    # stream; 1 step in 64 also carries that layer's tail write + commit).
-    pair_us = warm_ms * 1e3 / (K * nL)
-    pair_bytes = timed_bytes / (K * nL)
-    achieved = pair_bytes / (pair_us * 1e-6) / 1e9
+    # The decode launch (k_decode, one per layer: the FP8 stream, the tail,
+    # the fresh token's write and the merge) is the dominant work: its
+    # average duration is the timed region's span over its K * layers
+    # launches (events bracket the region on the kernels' own stream; 1 step
+    # in 64 also carries that layer's FP8 commit).
+    dec_us = warm_ms * 1e3 / (K * nL)
+    dec_bytes = timed_bytes / (K * nL)
+    achieved = dec_bytes / (dec_us * 1e-6) / 1e9
 
-    # ---- attribution within the pair: HIP events recorded by the decode loop
-    # before, between and after each layer's two launches (each event adds
-    # its own marker overhead, so these sum to more than pair_us)
+    # ---- the same launches one by one: HIP events recorded by the decode
+    # loop right before and after each layer's launch (each event adds its
+    # own marker overhead)
     nev = 3 * K * nL
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(nev)]
     for e in evs:  # the hipEvent_t handles exist once recorded
         e.record(stream)
     torch.cuda.synchronize()
     ev_arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs]) if nev else None
-    s_k = cur["step"]
     run(K, ev_arr)
     torch.cuda.synchronize()
-    att = [evs[3 * r].elapsed_time(evs[3 * r + 1]) for r in range(K * nL)]
-    fin = [evs[3 * r + 1].elapsed_time(evs[3 * r + 2]) for r in range(K * nL)]
-    att_us, fin_us = sum(att) / len(att) * 1e3, sum(fin) / len(fin) * 1e3
-    att_bytes = sum(attend_bytes(((ctx + i + 1) // 64) * 64) for i in range(s_k, s_k + K)) / K
-    log(f"decode pair: {pair_us:.2f} us per layer, {pair_bytes / 1e6:.2f} MB, {achieved:.0f} GB/s; "
-        f"event-bracketed: attend {att_us:.2f} us ({att_bytes / (att_us * 1e-6) / 1e9:.0f} GB/s), "
-        f"finish {fin_us:.2f} us")
+    one = sorted(evs[3 * r].elapsed_time(evs[3 * r + 1]) * 1e3 for r in range(K * nL))
+    ev_us = one[len(one) // 2]
+    log(f"decode launch: {dec_us:.2f} us per layer, {dec_bytes / 1e6:.2f} MB, {achieved:.0f} GB/s; "
+        f"event-bracketed median {ev_us:.2f} us")
+
+    # ---- measured ceiling: a plain streaming read of the same layers'
+    # committed FP8 K and V, one launch per layer, the same count of
+    # back-to-back launches as the timed region
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def plain_read(n_tok):
+        for _ in range(n_tok):
+            for i, L in enumerate(layers):
+                nb = arr[i].committed * NKV * D  # (arr holds the live copies)
+                call("cia_stream_read", L.kc8.data_ptr(), L.vc8.data_ptr(), nb, sink.data_ptr(),
+                     stream.cuda_stream)
+
+    plain_read(2)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    plain_read(K)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    floor_us = e0.elapsed_time(e1) * 1e3 / (K * nL)
+    floor_bytes = 2 * arr[0].committed * NKV * D
+    floor_gbps = floor_bytes / (floor_us * 1e-6) / 1e9
+    log(f"plain read of the same bytes: {floor_us:.2f} us per layer, {floor_gbps:.0f} GB/s "
+        f"({dec_us / floor_us:.2f}x the decode launch's time)")
 
     # ---- cold: evict the KV from the 256 MB Infinity Cache before every token
     # by reading 1 GiB of other data (a read leaves no dirty lines behind)
@@ -203,11 +218,24 @@ def main():
         c1.record(stream)
         torch.cuda.synchronize()
         cold.append(c0.elapsed_time(c1) * 1e3)
+    # the plain read, cold the same way (one token's worth of launches)
+    floor_cold = []
+    for _ in range(a.cold_steps if cold else 0):
+        flush.sum()
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        plain_read(1)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        floor_cold.append(c0.elapsed_time(c1) * 1e3)
     del flush
     cold.sort()
+    floor_cold.sort()
     cold_us = cold[len(cold) // 2] if cold else None
+    floor_cold_us = floor_cold[len(floor_cold) // 2] if floor_cold else None
     if cold:
-        log(f"cold: median {cold_us:.2f} us/token")
+        log(f"cold: median {cold_us:.2f} us/token; plain read cold {floor_cold_us:.2f} us/token")
     mean_tok_bytes = timed_bytes / K
 
     # ---- QK producers fused: the same layers take raw q / k, and the decode
@@ -236,8 +264,8 @@ def main():
             arr[l].prep_cap = 0
         prep = {"us_per_token": round(prep_us, 2), "tokens": n,
                 "over_prepared_inputs_us": round(prep_us - us_tok, 2),
-                "kernels": "producers inside k_decode_attend (prepared rows stored for "
-                             "k_decode_finish)"}
+                "kernels": "producers inside k_decode (q rows normalised in LDS, fresh k "
+                           "by the tail waves)"}
         log(f"decode with fused QK producers: {prep_us:.2f} us/token "
             f"({prep_us - us_tok:+.2f} against prepared inputs)")
 
@@ -308,8 +336,8 @@ def main():
                                         "out_proj_residual": round(med[2], 2)},
                  "int4_weight_bytes_per_layer": wbytes,
                  "launches_per_layer": 4,
-                 "kernels": "k_gemv_int4 (q/k/v), k_decode_attend + k_decode_finish "
-                            "(producers inside), k_gemv_int4 (out_proj + residual)"}
+                 "kernels": "k_gemv_int4 (q/k/v), k_decode (producers inside), "
+                            "k_gemv_int4 (out_proj + residual)"}
         log(f"attention branch (INT4 projections + attention): {blk_us:.2f} us/token; "
             f"per layer qkv {med[0]:.2f} / attention {med[1]:.2f} / out_proj {med[2]:.2f} us")
 
@@ -431,6 +459,17 @@ def main():
         cpu = cpu_baseline(cpu_layer, cpu_committed, ctx + cur["step"] - 1, q, nL,
                            a.cpu_seconds, log)
 
+    cpu_prefill = cpu_h2o = None
+    if not a.no_cpu:
+        if a.prefill > 0:
+            cpu_prefill = cpu_prefill_baseline(a.prefill, a.cpu_seconds, log)
+        if a.h2o_steps > 0:
+            cpu_h2o = cpu_h2o_baseline(a.cpu_seconds, log)
+    if prefill is not None:
+        prefill["cpu_baseline"] = cpu_prefill
+    if h2o is not None:
+        h2o["cpu_baseline"] = cpu_h2o
+
     traffic = a.traffic if a.traffic is not None else measured_traffic(ctx, nL)
     res = {
         "metric": "decode-attn µs/token + HBM GB/s (% of 8 TB/s) at 32k ctx; prefill MFMA util",
@@ -443,11 +482,11 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (fp8-e4m3/fp16 cache, f32 accumulate)",
+        "dtype": "fp16 MFMA operands (P in fp16), fp32 accumulate; FP8-E4M3/fp16 cache",
         "data": "synthetic: seeded N(0,1), K/V 1% outliers x20, Q QK-RMSNorm+RoPE",
         "config": {"workload": f"flash-decoding, ctx {ctx}, {nL} attention layers/token, batch 1, "
                                f"32Q/8KV heads, d64, FP8 E4M3 group-64 KV + fp16 tail",
-                   "context": ctx, "layers": nL, "decode": "matrix-core attend + finish"
+                   "context": ctx, "layers": nL, "decode": "matrix-core, one launch per layer"
                    if a.nsplit == 0 else f"split+combine nsplit={a.nsplit}"},
         "effective_gbps_warm": round(timed_bytes / (warm_ms * 1e-3) / 1e9, 1),
         "cold_us_per_token": round(cold_us, 3) if cold_us else None,
@@ -455,11 +494,18 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": "decode launch pair k_decode_attend + k_decode_finish",
-                     "algo_bytes_per_launch": int(pair_bytes),
-                     "avg_launch_us": round(pair_us, 3),
-                     "event_bracketed_us": {"k_decode_attend": round(att_us, 3),
-                                            "k_decode_finish": round(fin_us, 3)}},
+                     "traffic_source": TRAFFIC_FILE + " (not this run)" if traffic else None,
+                     "kernel": "k_decode (one launch per layer)",
+                     "algo_bytes_per_launch": int(dec_bytes),
+                     "avg_launch_us": round(dec_us, 3),
+                     "event_bracketed_median_us": round(ev_us, 3),
+                     "measured_ceiling": {
+                         "kernel": "k_stream_read (plain read of the same FP8 K+V, one "
+                                   "launch per layer)",
+                         "us_per_layer": round(floor_us, 3), "gbps": round(floor_gbps, 1),
+                         "frac": round(achieved / floor_gbps, 4),
+                         "cold_us_per_token": round(floor_cold_us, 3) if floor_cold_us else None,
+                         "cold_frac": round(floor_cold_us / cold_us, 4) if floor_cold_us else None}},
         "prefill": prefill,
         "qk_producers_fused": prep,
         "attention_branch": block,
@@ -473,14 +519,17 @@ def main():
 def long_context_leg(ctx, nL, steps, dev, stream, log):
     """Decode at ctx tokens (6 layers): the matrix-core path and the
     reference's split + combine with 16, 64, 256 and 512 splits per head.
-    Each setting: 2 warm-up tokens, then `steps` timed tokens."""
+    Each setting: 2 warm-up tokens, then `steps` timed tokens, then 2 tokens
+    with HIP events around each launch (split and combine separately); then
+    a plain streaming read of the same FP8 K+V, one launch per layer."""
     import ctypes
     import torch
     from cuda_inf_amd import _lib, workload
     from cuda_inf_amd.layer import AttnLayer
     from cuda_inf_amd._lib import D, NH, NKV, call
     settings = [0, 16, 64, 256, 512]
-    total = len(settings) * (steps + 2)
+    n_ev = 2
+    total = len(settings) * (steps + 2 + n_ev)
     layers = []
     for l in range(nL):
         L = AttnLayer(ctx + total + 64, nsplit=512, device=dev)
@@ -524,7 +573,49 @@ def long_context_leg(ctx, nL, steps, dev, stream, log):
         gbps = algo_bytes(Tc, ctx + cur - Tc) * nL / (us * 1e-6) / 1e9
         name = "matrix_core" if ns == 0 else f"split_{ns}"
         res[name] = {"us_per_token": round(us, 2), "gbps": round(gbps, 1)}
-        log(f"long context {ctx}: {name}: {us:.1f} us/token, {gbps:.0f} GB/s")
+        # events before, between (split | combine) and after each layer's launches
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * n_ev * nL)]
+        for e in evs:  # the hipEvent_t handles exist once recorded
+            e.record(stream)
+        torch.cuda.synchronize()
+        call("cia_decode_loop", arr, nL, q.data_ptr() + cur * qrow, kk.data_ptr() + cur * krow,
+             vv.data_ptr() + cur * krow, out.data_ptr() + cur * qrow, ctx + cur, n_ev, 0.125,
+             (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs]), stream.cuda_stream)
+        torch.cuda.synchronize()
+        cur += n_ev
+        first = sorted(evs[3 * r].elapsed_time(evs[3 * r + 1]) * 1e3 for r in range(n_ev * nL))
+        second = sorted(evs[3 * r + 1].elapsed_time(evs[3 * r + 2]) * 1e3 for r in range(n_ev * nL))
+        if ns == 0:
+            res[name]["launch_us_median"] = round(first[len(first) // 2], 2)
+            log(f"long context {ctx}: {name}: {us:.1f} us/token, {gbps:.0f} GB/s; "
+                f"one launch {first[len(first) // 2]:.1f} us")
+        else:
+            res[name]["split_us_median"] = round(first[len(first) // 2], 2)
+            res[name]["combine_us_median"] = round(second[len(second) // 2], 2)
+            log(f"long context {ctx}: {name}: {us:.1f} us/token, {gbps:.0f} GB/s; "
+                f"split {first[len(first) // 2]:.1f} us + combine {second[len(second) // 2]:.1f} us "
+                f"per layer (event-bracketed)")
+    # measured ceiling: the same committed FP8 K+V read plainly
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def plain_read(n_tok):
+        for _ in range(n_tok):
+            for i, L in enumerate(layers):
+                call("cia_stream_read", L.kc8.data_ptr(), L.vc8.data_ptr(),
+                     arr[i].committed * NKV * D, sink.data_ptr(), stream.cuda_stream)
+
+    plain_read(2)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    plain_read(steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    f_us = e0.elapsed_time(e1) * 1e3 / steps
+    f_gbps = 2 * arr[0].committed * NKV * D * nL / (f_us * 1e-6) / 1e9
+    res["plain_read"] = {"kernel": "k_stream_read", "us_per_token": round(f_us, 2),
+                         "gbps": round(f_gbps, 1),
+                         "matrix_core_frac": round(res["matrix_core"]["gbps"] / f_gbps, 4)}
+    log(f"long context {ctx}: plain read of the same bytes {f_us:.1f} us/token, {f_gbps:.0f} GB/s")
     return res
 
 
@@ -588,11 +679,10 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
 
 
 def measured_traffic(ctx: int, nL: int):
-    """HBM bytes per decode launch pair from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) when it was taken on
-    this workload; None otherwise."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                     "decode_pair_ctx32k_traffic.json")
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) when it was taken on this
+    workload; None otherwise."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
     try:
         with open(p) as f:
             t = json.load(f)
@@ -600,7 +690,7 @@ def measured_traffic(ctx: int, nL: int):
         return None
     if t.get("context") != ctx or t.get("layers") != nL:
         return None
-    return t.get("pair_bytes_per_launch")
+    return t.get("bytes_per_launch")
 
 
 def cpu_baseline(L, committed, qpos, q, nL, seconds, log):
@@ -645,6 +735,84 @@ def cpu_baseline(L, committed, qpos, q, nL, seconds, log):
             "sample": f"oracle split+combine (16 splits), one layer at {qpos + 1} keys, "
                       f"x{nL} layers; single-thread {res[1] * nL * 1e6:.0f} us/token; "
                       f"host {model} ({os.cpu_count()} cpus)"}
+
+
+def _host_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_prefill_baseline(S, seconds, log):
+    """The oracle's causal prefill (append with FP8 commit, then
+    attention_fused) for S tokens on one host core.  The append is timed
+    whole; the attention on the last query rows until about seconds / 2 have
+    passed, scaled to all S rows by (query, key) pairs."""
+    import numpy as np
+    import oracle
+    from cuda_inf_amd import workload
+    q, k, v = workload.qkv(S, seed=0, device="cpu")
+    qn, kn, vn = (t.view(torch_int16()).numpy().view(np.uint16) for t in (q, k, v))
+    ref = oracle.Group64Cache(S + 64)
+    t0 = time.perf_counter()
+    ref.append(kn, vn, 0)
+    t_app = time.perf_counter() - t0
+    # the last n rows in one call, n doubled until the call takes a quarter of
+    # the budget
+    n = 4
+    while True:
+        rows = list(range(S - n, S))
+        t0 = time.perf_counter()
+        oracle.attention_fused(qn, ref, S, 0, rows=rows)
+        t_att = time.perf_counter() - t0
+        if t_att > seconds / 4 or n >= S:
+            break
+        n = min(2 * n, S)
+    pairs = sum(r + 1 for r in rows)
+    full_pairs = S * (S + 1) // 2
+    att_full = t_att * full_pairs / pairs
+    total = t_app + att_full
+    log(f"cpu oracle prefill {S}: append {t_app * 1e3:.1f} ms + attention {att_full * 1e3:.0f} ms "
+        f"(scaled from {len(rows)} rows), 1 thread")
+    return {"value": round(total * 1e6, 1), "unit": "us/prefill", "cores": 1, "kind": "port",
+            "sample": f"oracle append of {S} tokens (whole) + attention_fused on the last "
+                      f"{len(rows)} query rows, scaled by (query, key) pairs to all {S} rows; "
+                      f"host {_host_model()}"}
+
+
+def cpu_h2o_baseline(seconds, log, C=2048, W=256, P=1024):
+    """The oracle's H2O layer (slot choice, per-token FP8 write, attention
+    with attn_sum) on one host core: a P-token prompt (untimed), then single
+    token steps for about seconds / 2."""
+    import numpy as np
+    import oracle
+    from cuda_inf_amd import workload
+    n = 4096 + P
+    g = workload.generator(7, "cpu")
+    q = workload.normal_f16((n, 32, 64), g, "cpu").view(torch_int16()).numpy().view(np.uint16)
+    k = workload.normal_f16((n, 8, 64), g, "cpu").view(torch_int16()).numpy().view(np.uint16)
+    v = workload.normal_f16((n, 8, 64), g, "cpu").view(torch_int16()).numpy().view(np.uint16)
+    hc = oracle.H2OCache(C, W)
+    hc.step(q[:P], k[:P], v[:P], 0, want_out=False)
+    steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2 and P + steps < n:
+        i = P + steps
+        hc.step(q[i:i + 1], k[i:i + 1], v[i:i + 1], i)
+        steps += 1
+    el = time.perf_counter() - t0
+    log(f"cpu oracle h2o C={C} W={W}: {el / steps * 1e6:.0f} us/step over {steps} steps, 1 thread")
+    return {"value": round(el / steps * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"oracle H2O steps {P}..{P + steps - 1} after a {P}-token prompt, "
+                      f"{C} slots, window {W}; host {_host_model()}"}
+
+
+def torch_int16():
+    import torch
+    return torch.int16
 
 
 if __name__ == "__main__":

@@ -164,6 +164,13 @@ int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
  * (also the size of a layer's ws_decode) */
 int64_t cia_decode_workspace_bytes(int max_tokens);
 
+/* A plain streaming read of `bytes` bytes at k and `bytes` at v (one
+ * layer's committed FP8 K and V), one launch: the measured memory ceiling
+ * the decode kernel is compared against.  No counterpart in the reference
+ * (a measurement utility).  bytes: a multiple of 16.  sink: one device
+ * uint32, written only on a checksum coincidence. */
+int cia_stream_read(const void* k, const void* v, int64_t bytes, uint32_t* sink, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* H2O eviction                                                       */
 /* ------------------------------------------------------------------ */
