@@ -41,6 +41,7 @@ SIGNATURES = {
     "cia_attn_decode": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, ctypes.c_int64, _P]),
     "cia_decode_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_stream_read": (_I, [_P, _P, ctypes.c_int64, _P, _P]),
+    "cia_attn_decode_noalloc": (_I, [_P] * 7 + [_I, _I, _F, _P, _P]),
     "cia_kv_quant_write": (_I, [_P] * 7 + [_I, _P]),
     "cia_h2o_place": (_I, [_P] * 10 + [_I, _I, _I, _I, _P]),
     "cia_attention_h2o": (_I, [_P] * 6 + [_I, _P, _P, _I, _I, _F, _P, ctypes.c_int64, _P]),

@@ -61,6 +61,7 @@
 //   - a device-scope atomic round trip: about 0.25 us idle, 0.4-0.5 us under
 //     the stream; the acknowledgement of agent-coherent stores about 0.6 us.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "attn_range.h"
@@ -745,4 +746,72 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
     }
   }
   return CIA_OK;
+}
+
+// ---------------------------------------------------------------- no allocation
+// cia_attn_decode's workspace as a file-scope device array: the entry below
+// allocates nothing.  Its arrival counters are zero at load; every complete
+// call leaves them at zero, and the first call on a device clears them once
+// more with a fill kernel.  Calls on one device share the array: calls that
+// overlap (different streams, or host threads) race.
+static __device__ __align__(256) uint8_t scratch[kWsBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];  // this device's address of `scratch`
+
+__global__ void k_zero_u32(uint32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+// the current device's copy of `scratch` (set up on its first call)
+int scratch_for_device(void** out, hipStream_t s) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_hip_error(e);
+    return CIA_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return CIA_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_hip_error(e);
+      return CIA_ERR_HIP;
+    }
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, s,
+                       (uint32_t*)((char*)p + kPartBytes), NKV * kCntStride);
+    const int st = launch_status();
+    if (st) return st;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return CIA_OK;
+}
+
+}  // namespace
+
+extern "C" int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                                       const uint16_t* ksc, const uint16_t* vsc,
+                                       const uint16_t* ktail, const uint16_t* vtail, int committed,
+                                       int qpos, float scale, uint16_t* out, void* stream) {
+  CIA_REQUIRE(q && kc8 && vc8 && ksc && vsc && ktail && vtail && out, CIA_ERR_NULL);
+  CIA_REQUIRE(committed >= 0 && committed % G == 0 && qpos >= 0, CIA_ERR_ARG);
+  CIA_REQUIRE(aligned(q, 16) && aligned(kc8, 16) && aligned(vc8, 16) && aligned(ktail, 16) &&
+                  aligned(vtail, 16) && aligned(ksc, 2) && aligned(vsc, 2) && aligned(out, 2),
+              CIA_ERR_ALIGN);
+  CIA_REQUIRE(committed <= qpos + 1 && qpos - committed < G, CIA_ERR_STATE);
+  // the workspace this context needs must fit the array (it does for every
+  // context: the partials are sized for the largest split)
+  CIA_REQUIRE(cia_decode_workspace_bytes(qpos + 1) <= (int64_t)sizeof(scratch), CIA_ERR_ARG);
+  void* ws = nullptr;
+  const int st = scratch_for_device(&ws, (hipStream_t)stream);
+  if (st) return st;
+  return cia_decode_mfma(q, kc8, vc8, ksc, vsc, (uint16_t*)ktail, (uint16_t*)vtail, nullptr,
+                         nullptr, committed, qpos, scale, out, ws, kWsBytes, stream, nullptr,
+                         nullptr);
 }

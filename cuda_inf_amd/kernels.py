@@ -138,6 +138,17 @@ def attn_decode(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int, 
          _dev(ws, "ws", (torch.uint8,), decode_workspace_bytes(qpos + 1)), ws.numel(), _stream())
 
 
+def attn_decode_noalloc(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int,
+                        scale: float, out) -> None:
+    """attn_decode with the library's own fixed workspace (allocates
+    nothing; calls overlapping on one GPU race)."""
+    call("cia_attn_decode_noalloc", _dev(q, "q", _F16, NH * D),
+         _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
+         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+         committed, qpos, float(scale), _dev(out, "out", _F16, NH * D), _stream())
+
+
 # ------------------------------------------------------------ H2O
 def kv_quant_write(k, v, kf, vf, ks, vs, dst_slots, S: int) -> None:
     """engine.cu:317-333: per-token FP8 quantisation into slots dst_slots[j]."""

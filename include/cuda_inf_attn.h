@@ -164,6 +164,20 @@ int cia_attn_decode(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
  * (also the size of a layer's ws_decode) */
 int64_t cia_decode_workspace_bytes(int max_tokens);
 
+/* cia_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a fixed device array inside the library (274 KiB per GPU,
+ * held until the process ends; it covers every context); the call allocates
+ * nothing.  Calls on one GPU share it: calls that overlap on one GPU
+ * (several streams or host threads) race.  Same arguments, results and
+ * errors as cia_attn_decode otherwise. */
+int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                            const uint16_t* ksc, const uint16_t* vsc,
+                            const uint16_t* ktail, const uint16_t* vtail,
+                            int committed, int qpos, float scale, uint16_t* out,
+                            void* stream);
+
 /* A plain streaming read of `bytes` bytes at k and `bytes` at v (one
  * layer's committed FP8 K and V), one launch: the measured memory ceiling
  * the decode kernel is compared against.  No counterpart in the reference
