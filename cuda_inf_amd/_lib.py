@@ -34,7 +34,7 @@ SIGNATURES = {
     "cia_e4m3_encode_range": (_I, [ctypes.c_uint32, ctypes.c_int64, _P, _P]),
     "cia_kv_write_tail": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "cia_kv_commit_group": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
-    "cia_attention_fused": (_I, [_P] * 7 + [_I, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_attention_fused": (_I, [_P] * 7 + [_I, _P, _P, _I, _I, _F, _P, ctypes.c_int64, _P]),
     "cia_attention_fused_fp8": (_I, [_P] * 7 + [_I, _P, _I, _I, _F, _P]),
     "cia_attn_decode_split": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I, _P]),
     "cia_attn_decode_combine": (_I, [_P, _P, _P, _P, _I, _P]),

@@ -140,8 +140,8 @@ extern "C" int cia_attention_fused(const uint16_t* q, const uint8_t* kc8, const 
                                    const uint16_t* ksc, const uint16_t* vsc,
                                    const uint16_t* ktail, const uint16_t* vtail, int committed,
                                    uint16_t* out, float* attn_sum, int S, int past, float scale,
-                                   void* ws, void* stream) {
-  CIA_REQUIRE(S >= 0 && past >= 0, CIA_ERR_ARG);
+                                   void* ws, int64_t ws_bytes, void* stream) {
+  CIA_REQUIRE(S >= 0 && past >= 0 && ws_bytes >= 0, CIA_ERR_ARG);
   if (S == 0) return CIA_OK;
   int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
   if (st) return st;
@@ -149,6 +149,11 @@ extern "C" int cia_attention_fused(const uint16_t* q, const uint8_t* kc8, const 
   CIA_REQUIRE(aligned(out, 2), CIA_ERR_ALIGN);
   CIA_REQUIRE(past + S - 1 - committed < G, CIA_ERR_STATE);
   CIA_REQUIRE(scale >= 0.0f && scale < __builtin_inff(), CIA_ERR_ARG);
+  if (attn_sum) {
+    CIA_REQUIRE(ws, CIA_ERR_NULL);
+    CIA_REQUIRE(aligned(attn_sum, 4) && aligned(ws, 16), CIA_ERR_ALIGN);
+    CIA_REQUIRE(ws_bytes >= cia_mass_workspace_bytes(S), CIA_ERR_ARG);
+  }
   st = cia_prefill_mfma(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, out, S, past, scale,
                         stream);
   if (st || !attn_sum) return st;

@@ -254,7 +254,7 @@ int group64_attend(cia_layer* L, const uint16_t* q, uint16_t* out, int S, int pa
                            cia_decode_workspace_bytes(L->maxT), stream, mid_event, nullptr);
   }
   int st = cia_attention_fused(q, L->kc8, L->vc8, L->ksc, L->vsc, L->ktail, L->vtail,
-                               L->committed, out, nullptr, S, past, scale, nullptr, stream);
+                               L->committed, out, nullptr, S, past, scale, nullptr, 0, stream);
   if (st) return st;
   if (mid_event) return hip_check(hipEventRecord((hipEvent_t)mid_event, (hipStream_t)stream));
   return CIA_OK;

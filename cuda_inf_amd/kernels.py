@@ -77,7 +77,7 @@ def attention_fused(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out, at
          committed, _dev(out, "out", _F16, S * NH * D),
          _opt(attn_sum, "attn_sum", (torch.float32,), T), S, past, float(scale),
          _opt(ws, "ws", None, mass_workspace_bytes(S) if attn_sum is not None else None),
-         _stream())
+         ws.numel() * ws.element_size() if ws is not None else 0, _stream())
 
 
 def attention_fused_fp8(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out, S: int,

@@ -104,13 +104,14 @@ int cia_e4m3_encode_range(uint32_t first_bits, int64_t n, uint8_t* out,
  * over FP8 keys [0, min(committed, qpos+1)) and tail keys up to qpos.
  * out [S][32][64] fp16.  attn_sum (may be NULL): per-key attention mass is
  * added with the deterministic rule of cia_attention_h2o; it then needs
- * `ws` of cia_mass_workspace_bytes(S) bytes (else ws may be NULL). */
+ * `ws` of ws_bytes >= cia_mass_workspace_bytes(S) bytes (else ws may be NULL
+ * and ws_bytes 0); a smaller ws is rejected with CIA_ERR_ARG. */
 int cia_attention_fused(const uint16_t* q, const uint8_t* kc8,
                         const uint8_t* vc8, const uint16_t* ksc,
                         const uint16_t* vsc, const uint16_t* ktail,
                         const uint16_t* vtail, int committed, uint16_t* out,
                         float* attn_sum, int S, int past, float scale,
-                        void* ws, void* stream);
+                        void* ws, int64_t ws_bytes, void* stream);
 
 /* The causal attention of attention_fused (engine.cu:236-308) with both
  * products on the OCP-fp8 matrix cores (no counterpart kernel in the

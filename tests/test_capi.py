@@ -57,9 +57,13 @@ FAKE = 0x10000  # aligned non-null address: validation must fail before any use
     (lambda L: L.cia_attn_decode_combine(FAKE, FAKE, FAKE, FAKE, 0, None), 3),
     (lambda L: L.cia_attn_decode(*([FAKE] * 7), 128, 100, 0.125, FAKE, FAKE, 1 << 20, None), 5),
     (lambda L: L.cia_attn_decode(*([FAKE] * 7), 64, 100, 0.125, FAKE, None, 1 << 20, None), 1),
-    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, None, 10, 100, 0.125, None, None), 5),
-    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, None, -1, 0, 0.125, None, None), 3),
-    (lambda L: L.cia_attention_fused(*([None] * 7), 0, None, None, 0, 0, 0.125, None, None), 0),
+    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, None, 10, 100, 0.125, None, 0, None), 5),
+    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, None, -1, 0, 0.125, None, 0, None), 3),
+    (lambda L: L.cia_attention_fused(*([None] * 7), 0, None, None, 0, 0, 0.125, None, 0, None), 0),
+    # attn_sum needs a mass workspace of cia_mass_workspace_bytes(S) bytes
+    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, FAKE, 10, 0, 0.125, None, 0, None), 1),
+    (lambda L: L.cia_attention_fused(*([FAKE] * 7), 0, FAKE, FAKE, 10, 0, 0.125, FAKE,
+                                     10 * 32 * 2 * 4 - 4, None), 3),
     (lambda L: L.cia_kv_quant_write(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 3, None), 1),
     (lambda L: L.cia_kv_quant_write(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, None), 3),
     (lambda L: L.cia_attention_h2o(*([FAKE] * 6), 0, FAKE, FAKE, 1, 0, 0.125, FAKE, 1 << 20, None), 3),

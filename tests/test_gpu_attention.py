@@ -237,7 +237,7 @@ def test_decode_loop_two_layers_through_commit(orc, cia, dev):
     v = torch.stack(vs).contiguous()
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     out = torch.empty_like(qd)
-    # three calls (graph replays after the first capture), eager work between
+    # three eager calls, with other work and a synchronisation between them
     qrow, krow = nL * 32 * 64 * 2, nL * 8 * 64 * 2
     s0 = 0
     for n in (25, 20, 25):
@@ -272,9 +272,10 @@ def test_decode_loop_two_layers_through_commit(orc, cia, dev):
 def test_prefill_fp8_error(orc, cia, dev, S, past, outliers):
     """The OCP-fp8 matrix-core prefill on the same cache as the fp16 kernel:
     its error against the fp32 restatement, with Q and the softmax
-    numerators rounded to fp8, is printed and bounded loosely (mean absolute
-    error below 0.01, max below 0.1); the fp16 kernel stays within
-    2e-3 + 1e-3|ref|."""
+    numerators rounded to fp8, is printed and bounded at about twice the
+    measured error of its input class (measured on MI355X: without outliers
+    max 0.0012, mean 6e-5; with outliers max 0.042, mean 3e-4); the fp16
+    kernel's output of the same layer stays within 2e-3 + 1e-3|ref|."""
     from cuda_inf_amd import kernels as K
     from cuda_inf_amd.layer import AttnLayer
     from cuda_inf_amd.workload import qkv
@@ -286,7 +287,7 @@ def test_prefill_fp8_error(orc, cia, dev, S, past, outliers):
         ref.append(_u16(k0), _u16(v0), 0)
     q, k, v = qkv(S, seed=12, device="cpu", past=past, outliers=outliers)
     qd = q.to(dev)
-    L.forward(qd, k.to(dev), v.to(dev), past)
+    out16, _ = L.forward(qd, k.to(dev), v.to(dev), past)
     ref.append(_u16(k), _u16(v), past)
     out8 = torch.empty_like(qd)
     print(f"prefill fp8 S={S} past={past}", flush=True)
@@ -299,10 +300,13 @@ def test_prefill_fp8_error(orc, cia, dev, S, past, outliers):
                                          np.arange(0, S, 37)])).astype(np.int32)
     _, r32 = orc.attention_fused(_u16(q), ref, S, past, rows=rows)
     got = out8.float().cpu().numpy()
+    g16 = _u16(out16)
     if rows is not None:
-        got, r32 = got[rows], r32[rows]
+        got, r32, g16 = got[rows], r32[rows], g16[rows]
+    assert_close_f16(g16, r32, what="fp16 prefill")
     err = np.abs(got - r32)
     print(f"fp8 prefill S={S} past={past}: max abs err {err.max():.4g}, mean {err.mean():.4g}, "
           f"max rel {(err / (np.abs(r32) + 1e-3)).max():.3g}")
     assert np.isfinite(got).all()
-    assert err.mean() < 0.01 and err.max() < 0.1
+    max_bound, mean_bound = (0.08, 7e-4) if outliers else (0.003, 2e-4)
+    assert err.max() <= max_bound and err.mean() <= mean_bound

@@ -1,0 +1,220 @@
+"""Parity at the benchmark's sizes and on the remaining entry-point options:
+
+- attention_fused with attn_sum (engine.cu:291-307): the accumulated mass bit
+  for bit against the oracle (S > 1, past > 0, a tail, outliers, a non-zero
+  starting attn_sum);
+- cia_decode_loop at 32 768 keys, 2 layers, across the group boundary at
+  32 768: every step's output within tolerance and the committed group and
+  tail bytes identical, once with prepared q/k and once with the QK
+  producers inside the decode kernel;
+- the reference's split + combine at 131 072 keys, 16 and 512 splits: the
+  output and the partials;
+- one 4096-token append: every committed byte and scale and the tail.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev).view(torch.float16)
+
+
+def _append(L, k, v, past, dev):
+    from cuda_inf_amd._lib import call
+    kd, vd = k.to(dev), v.to(dev)
+    call("cia_layer_append", ctypes.byref(L._s), kd.data_ptr(), vd.data_ptr(), k.shape[0], past,
+         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+
+
+def test_attention_fused_attn_sum_bit_exact(orc, cia, dev):
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    past, S = 1000, 150  # keys 0..1149: 17 committed groups, then a 62-key tail
+    L = AttnLayer(past + S + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(past + S + 64)
+    _, k0, v0 = qkv(past, seed=41, device="cpu", outliers=True)
+    _append(L, k0, v0, 0, dev)
+    ref.append(_u16(k0), _u16(v0), 0)
+    q, k, v = qkv(S, seed=42, device="cpu", past=past, outliers=True)
+    _append(L, k, v, past, dev)
+    ref.append(_u16(k), _u16(v), past)
+    assert L.committed == ref.committed == 1088
+    T = past + S
+    start = np.linspace(0.5, 3.0, T).astype(np.float32)  # accumulation onto existing mass
+    asum = torch.from_numpy(start.copy()).to(dev)
+    ws = torch.empty(K.mass_workspace_bytes(S), dtype=torch.uint8, device=dev)
+    out = torch.empty((S, 32, 64), dtype=torch.float16, device=dev)
+    K.attention_fused(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed, out,
+                      asum, S, past, 0.125, ws)
+    torch.cuda.synchronize()
+    rsum = start.copy()
+    _, r32 = orc.attention_fused(_u16(q), ref, S, past, attn_sum=rsum)
+    got = asum.cpu().numpy()
+    bad = np.nonzero(got.view(np.uint32) != rsum.view(np.uint32))[0]
+    assert bad.size == 0, (f"{bad.size} of {T} attn_sum entries differ; first at {bad[0]}: "
+                           f"{got[bad[0]]!r} vs {rsum[bad[0]]!r}")
+    assert_close_f16(_u16(out), r32)
+
+
+def test_attention_fused_rejects_small_mass_workspace(cia, dev):
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd._lib import call, CiaError
+    from cuda_inf_amd.layer import AttnLayer
+    L = AttnLayer(256, nsplit=16, device=dev)
+    S = 40
+    q = torch.zeros((S, 32, 64), dtype=torch.float16, device=dev)
+    out = torch.empty_like(q)
+    asum = torch.zeros(S, dtype=torch.float32, device=dev)
+    ws = torch.empty(K.mass_workspace_bytes(S) - 16, dtype=torch.uint8, device=dev)
+    with pytest.raises(CiaError):
+        call("cia_attention_fused", q.data_ptr(), L.kc8.data_ptr(), L.vc8.data_ptr(),
+             L.ksc.data_ptr(), L.vsc.data_ptr(), L.ktail.data_ptr(), L.vtail.data_ptr(), 0,
+             out.data_ptr(), asum.data_ptr(), S, 0, 0.125, ws.data_ptr(), ws.numel(),
+             torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("producers", [False, True])
+def test_decode_loop_32k_two_layers_through_commit(orc, cia, dev, producers):
+    from cuda_inf_amd import _lib, workload
+    from cuda_inf_amd.layer import AttnLayer
+    nL, n0, steps = 2, 32768 - 5, 12  # tail 59 keys; the step at 32767 commits group 511
+    rng = np.random.default_rng(7)
+    qw = rng.uniform(0.5, 1.5, 64).astype(np.float16)
+    kw = rng.uniform(0.5, 1.5, 64).astype(np.float16)
+    layers, refs = [], []
+    for l in range(nL):
+        L = AttnLayer(n0 + steps + 64, nsplit=0, device=dev)
+        ref = orc.Group64Cache(n0 + steps + 64)
+        _, k0, v0 = workload.qkv(n0, seed=60 + l, device="cpu", outliers=True)
+        _append(L, k0, v0, 0, dev)
+        ref.append(_u16(k0), _u16(v0), 0)
+        layers.append(L)
+        refs.append(ref)
+    print(f"decode loop 32k, producers={producers}: caches built", flush=True)
+    arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+    pos = np.arange(n0, n0 + steps, dtype=np.int32)
+    qs, ks, vs, pqs, pks = [], [], [], [], []
+    for l in range(nL):
+        g = np.random.default_rng(100 + l)
+        qr = (g.standard_normal((steps, 32, 64)) * 2).astype(np.float16)
+        kr = (g.standard_normal((steps, 8, 64)) * 2).astype(np.float16)
+        vr = g.standard_normal((steps, 8, 64)).astype(np.float16)
+        if producers:
+            pq, pk = orc.qk_norm_rope(qr, kr, qw, kw, pos)
+            qs.append(qr.view(np.uint16))
+            ks.append(kr.view(np.uint16))
+        else:
+            # prepared inputs: the producers' output itself
+            pq, pk = orc.qk_norm_rope(qr, kr, qw, kw, pos)
+            qs.append(pq)
+            ks.append(pk)
+        pqs.append(pq)
+        pks.append(pk)
+        vs.append(vr.view(np.uint16))
+    q = np.stack(qs, 1)  # [steps, nL, 32, 64]
+    k = np.stack(ks, 1)
+    v = np.stack(vs, 1)
+    qd, kd, vd = _t16(q, dev), _t16(k, dev), _t16(v, dev)
+    keep = []
+    if producers:
+        qwd, kwd = _t16(qw, dev), _t16(kw, dev)
+        keep += [qwd, kwd]
+        for l in range(nL):
+            pw = torch.zeros((32 + 8) * 64, dtype=torch.float16, device=dev)
+            keep.append(pw)
+            arr[l].qw, arr[l].kw = qwd.data_ptr(), kwd.data_ptr()
+            arr[l].eps, arr[l].theta = workload.EPS, workload.ROPE_THETA
+            arr[l].prep_ws, arr[l].prep_cap = pw.data_ptr(), 1
+    out = torch.empty((steps, nL, 32, 64), dtype=torch.float16, device=dev)
+    _lib.call("cia_decode_loop", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+              out.data_ptr(), n0, steps, 0.125, None, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = _u16(out)
+    for s in range(steps):
+        p = n0 + s
+        for l in range(nL):
+            refs[l].append(pks[l][s:s + 1], vs[l][s:s + 1], p)
+            _, r32, _ = orc.attn_decode(pqs[l][s], refs[l], p, nsplit=16, nthreads=8)
+            assert_close_f16(got[s, l], r32, what=f"step {s} (key {p}) layer {l}")
+    for l in range(nL):
+        c = refs[l].committed
+        assert c == 32768 and arr[l].committed == c
+        L = layers[l]
+        lo = 0
+        assert np.array_equal(L.kc8.cpu().numpy().reshape(-1)[lo:c * 512],
+                              refs[l].kc8.reshape(-1)[lo:c * 512])
+        assert np.array_equal(L.vc8.cpu().numpy().reshape(-1)[lo:c * 512],
+                              refs[l].vc8.reshape(-1)[lo:c * 512])
+        assert np.array_equal(_u16(L.ksc).reshape(-1)[:c // 64 * 8], refs[l].ksc.reshape(-1)[:c // 64 * 8])
+        assert np.array_equal(_u16(L.vsc).reshape(-1)[:c // 64 * 8], refs[l].vsc.reshape(-1)[:c // 64 * 8])
+        nt = n0 + steps - c
+        assert np.array_equal(_u16(L.ktail).reshape(64, -1)[:nt], refs[l].ktail.reshape(64, -1)[:nt])
+        assert np.array_equal(_u16(L.vtail).reshape(64, -1)[:nt], refs[l].vtail.reshape(64, -1)[:nt])
+
+
+@pytest.fixture(scope="module")
+def cache131k(orc, dev):
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    n = 131072
+    L = AttnLayer(n + 64, nsplit=512, device=dev)
+    ref = orc.Group64Cache(n + 64)
+    for c0 in range(0, n, 16384):
+        _, k, v = qkv(16384, seed=900 + c0 // 16384, device="cpu", past=c0, outliers=True)
+        _append(L, k, v, c0, dev)
+        ref.append(_u16(k), _u16(v), c0)
+    assert L.committed == ref.committed == n
+    return L, ref
+
+
+@pytest.mark.parametrize("nsplit", [16, 512])
+def test_split_combine_131k(orc, cia, dev, cache131k, nsplit):
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.workload import qkv
+    L, ref = cache131k
+    qpos = 131071
+    q, _, _ = qkv(1, seed=77 + nsplit, device="cpu", past=qpos)
+    pm = torch.zeros(32 * nsplit, device=dev)
+    pl = torch.zeros(32 * nsplit, device=dev)
+    po = torch.zeros(32 * nsplit * 64, device=dev)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    K.attn_decode_split(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed,
+                        qpos, 0.125, pm, pl, po, nsplit)
+    K.attn_decode_combine(pm, pl, po, out, nsplit)
+    torch.cuda.synchronize()
+    _, r32, (rpm, rpl, rpo) = orc.attn_decode(_u16(q), ref, qpos, nsplit=nsplit, nthreads=8)
+    assert_close_f16(_u16(out), r32)
+    np.testing.assert_allclose(pm.cpu().numpy(), rpm, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(pl.cpu().numpy(), rpl, rtol=2e-4)
+    np.testing.assert_allclose(po.cpu().numpy().reshape(rpo.shape), rpo, rtol=2e-3, atol=2e-3)
+
+
+def test_append_4096_bit_exact(orc, cia, dev):
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    S = 4096
+    L = AttnLayer(S + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(S + 64)
+    _, k, v = qkv(S, seed=5, device="cpu", outliers=True)
+    _append(L, k, v, 0, dev)
+    ref.append(_u16(k), _u16(v), 0)
+    assert L.committed == ref.committed == S
+    assert np.array_equal(L.kc8.cpu().numpy(), ref.kc8)
+    assert np.array_equal(L.vc8.cpu().numpy(), ref.vc8)
+    assert np.array_equal(_u16(L.ksc), ref.ksc)
+    assert np.array_equal(_u16(L.vsc), ref.vsc)
+    assert np.array_equal(_u16(L.ktail), ref.ktail)
+    assert np.array_equal(_u16(L.vtail), ref.vtail)

@@ -189,6 +189,35 @@ def test_fused_invariants(orc):
         np.testing.assert_allclose(o0[i], np.repeat(mean, 4, axis=0), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("S,past", [(40, 100), (70, 0), (1, 63)])
+def test_fused_attn_sum_against_fp64(orc, S, past):
+    """attention_fused's attn_sum (oracle.c:488-491, engine.cu:291-307): the
+    mass each key receives, summed over the S queries and 32 heads, added
+    onto the existing values; against softmax in fp64 on the dequantised
+    cache, and the total added is S * 32 (each softmax sums to 1)."""
+    rng = np.random.default_rng(100 + S + past)
+    c, _, _ = make_cache(orc, rng, past + S)
+    q = rand_f16(rng, (S, NH, D))
+    T = past + S
+    start = rng.uniform(0.0, 5.0, T).astype(np.float32)
+    asum = start.copy()
+    orc.attention_fused(bits(q), c, S, past, attn_sum=asum)
+    K, V = dequant_cache(c, T)
+    mass = np.zeros(T)
+    for i in range(S):
+        n = past + i + 1
+        for h in range(NH):
+            sc = (K[:n, h // 4] @ q[i, h].astype(np.float64)) * 0.125
+            p = np.exp(sc - sc.max())
+            mass[:n] += p / p.sum()
+    added = asum.astype(np.float64) - start.astype(np.float64)
+    # S * 32 fp32 adds per key into accumulators up to ~S * 32: rounding ~1e-7 relative each
+    np.testing.assert_allclose(added, mass, rtol=1e-4, atol=2e-5 * S)
+    assert abs(added.sum() - S * NH) < 1e-3 * S
+    # keys no query can see (none here) and the visible ones: every key got mass
+    assert np.all(added > 0)
+
+
 def test_decode_equals_fused_last_row_and_splits_agree(orc):
     rng = np.random.default_rng(13)
     n = 1000  # 15 groups + 40 tail keys
