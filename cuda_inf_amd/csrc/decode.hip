@@ -40,34 +40,73 @@ __global__ __launch_bounds__(256) void k_decode_split(const uint16_t* __restrict
   }
 }
 
-// engine.cu:467-480 with runtime nsplit; grid = 32 heads, block = 64 dims
-__device__ __forceinline__ float combine_one(const float* pm, const float* pl, const float* po,
-                                             int h, int d, int nsplit) {
-  float gm = -1e30f;
-  for (int s = 0; s < nsplit; s++) gm = __builtin_fmaxf(gm, pm[h * nsplit + s]);
-  float l = 0.f, acc = 0.f;
-  for (int s = 0; s < nsplit; s++) {
-    const int pi = h * nsplit + s;
-    const float ls = pl[pi];
-    if (ls <= 0.f) continue;
-    const float w = fast_exp(pm[pi] - gm);
-    l = __builtin_fmaf(ls, w, l);
-    acc = __builtin_fmaf(po[(size_t)pi * D + d], w, acc);
-  }
-  return acc / l;
-}
+// engine.cu:467-480 with runtime nsplit: the same merge (global max over the
+// splits' m, splits with l <= 0 skipped, exp weights), spread over 4 blocks
+// per query head (16 dims each) of 1024 threads: thread (group j, lane e)
+// sums splits j, j + 64, ... of dim 16 (blockIdx.y) + e, then the 64 sums
+// are added in LDS.  grid = (32 heads, 4).
+constexpr int kCombThreads = 1024;
+constexpr int kCombDims = 16;
+constexpr int kCombGroups = kCombThreads / kCombDims;
 
-__global__ __launch_bounds__(64) void k_decode_combine(const float* __restrict__ pm,
-                                                       const float* __restrict__ pl,
-                                                       const float* __restrict__ po,
-                                                       uint16_t* __restrict__ out, int nsplit) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  out[h * D + d] = f2h(combine_one(pm, pl, po, h, d, nsplit));
+__global__ __launch_bounds__(kCombThreads) void k_decode_combine(const float* __restrict__ pm,
+                                                                 const float* __restrict__ pl,
+                                                                 const float* __restrict__ po,
+                                                                 uint16_t* __restrict__ out,
+                                                                 int nsplit) {
+  __shared__ float sacc[kCombGroups * kCombDims];
+  __shared__ float sred[kCombThreads / 64];
+  __shared__ float sl[kCombGroups];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int e = tid % kCombDims, j = tid / kCombDims, d = blockIdx.y * kCombDims + e;
+  const float* hm = pm + (size_t)h * nsplit;
+  const float* hl = pl + (size_t)h * nsplit;
+  const float* ho = po + (size_t)h * nsplit * D;
+  float gm = -1e30f;
+  for (int s = tid; s < nsplit; s += kCombThreads) gm = __builtin_fmaxf(gm, hm[s]);
+  gm = wave_max(gm);
+  if ((tid & 63) == 0) sred[tid >> 6] = gm;
+  __syncthreads();
+  gm = sred[0];
+#pragma unroll
+  for (int k = 1; k < kCombThreads / 64; k++) gm = __builtin_fmaxf(gm, sred[k]);
+  float l = 0.f, acc = 0.f;
+#pragma unroll 4
+  for (int s = j; s < nsplit; s += kCombGroups) {
+    const float ls = hl[s];
+    if (ls <= 0.f) continue;
+    const float w = fast_exp(hm[s] - gm);
+    l = __builtin_fmaf(ls, w, l);
+    acc = __builtin_fmaf(ho[(size_t)s * D + d], w, acc);
+  }
+  sacc[j * kCombDims + e] = acc;
+  if (e == 0) sl[j] = l;
+  __syncthreads();
+  if (tid < kCombDims) {
+    float L = 0.f, A = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < kCombGroups; k++) {
+      L += sl[k];
+      A += sacc[k * kCombDims + tid];
+    }
+    out[h * D + blockIdx.y * kCombDims + tid] = f2h(A / L);
+  }
 }
 
 }  // namespace cia
 
 using namespace cia;
+
+// The matrix-core split runs for up to 512 splits per head of at least 128
+// keys each.  Smaller splits take the fp32 kernel above: the matrix cores
+// round the softmax numerators to fp16, and a split's own output o / l over
+// a handful of keys (with outlier values) would carry that rounding unaveraged.
+constexpr int kSplitMfmaMax = 512;
+constexpr int kSplitMfmaMinKeys = 128;
+extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed, int qpos,
+    float scale, float* pm, float* pl, float* po, int nsplit, void* stream);
 
 static int check_cache(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                        const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
@@ -90,6 +129,9 @@ extern "C" int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8, cons
   CIA_REQUIRE(pm && pl && po, CIA_ERR_NULL);
   CIA_REQUIRE(qpos >= 0 && nsplit >= 1 && nsplit <= CIA_NSPLIT_MAX, CIA_ERR_ARG);
   CIA_REQUIRE(qpos - committed < G, CIA_ERR_STATE);  // the tail holds at most 64 keys
+  if (nsplit <= kSplitMfmaMax && (qpos + nsplit) / nsplit >= kSplitMfmaMinKeys)
+    return cia_split_mfma(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, qpos, scale, pm, pl, po,
+                          nsplit, stream);
   Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
   hipLaunchKernelGGL(k_decode_split, dim3(NKV, nsplit), dim3(256), 0, (hipStream_t)stream, q, c,
                      qpos, scale, pm, pl, po, nsplit);
@@ -100,8 +142,8 @@ extern "C" int cia_attn_decode_combine(const float* pm, const float* pl, const f
                                        uint16_t* out, int nsplit, void* stream) {
   CIA_REQUIRE(pm && pl && po && out, CIA_ERR_NULL);
   CIA_REQUIRE(nsplit >= 1 && nsplit <= CIA_NSPLIT_MAX, CIA_ERR_ARG);
-  hipLaunchKernelGGL(k_decode_combine, dim3(NH), dim3(D), 0, (hipStream_t)stream, pm, pl, po,
-                     out, nsplit);
+  hipLaunchKernelGGL(k_decode_combine, dim3(NH, D / kCombDims), dim3(kCombThreads), 0,
+                     (hipStream_t)stream, pm, pl, po, out, nsplit);
   return launch_status();
 }
 

@@ -96,6 +96,7 @@ constexpr int kPartRow = 4 + D;            // one head's partial: m, l, -, -, o[
 constexpr int kPartF = GQA * kPartRow;     // floats of one workgroup partial
 constexpr int kCntStride = 64;             // uint32 between the kv heads' counters (256 B)
 constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
 constexpr int64_t kPartBytes = (int64_t)NKV * kMaxRanges * kPartF * sizeof(float);
 constexpr int64_t kWsBytes = kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
 
@@ -172,12 +173,26 @@ struct DecArgs {
   int ne;                // extra groups: the last ne groups, one each to wave 8
                          // of workgroups 1..ne
   QkPrep prep;
+  // split mode (the reference's attn_decode_split partials, committed keys only)
+  float* pm;             // [32][nsplit] max score (natural units), -1e30 when empty
+  float* pl;             // [32][nsplit] sum of exp(s - m)
+  float* po;             // [32][nsplit][64] sum of exp(s - m) v
+  int nsplit, chunk, total;
 };
 
 // ---------------------------------------------------------------- kernel
 // grid = 8R, block = kDecThreads.  kPrep: q (and the fresh k) arrive raw and
 // the QK producers (engine.cu:799-801) run here.
-template <bool kPrep>
+// kSplit: the committed keys of the reference's splits (attn_decode_split,
+// engine.cu:396-465; split s covers keys [s chunk, (s + 1) chunk) of the
+// qpos + 1): workgroup r of kv head g takes splits [r nsplit / R,
+// (r + 1) nsplit / R); its FP8 waves share a split's groups when it has at
+// most 8 splits, else take whole splits, and each finished split (or share)
+// is written as (m, l, o) -- straight to pm / pl / po when the workgroup has
+// 8 splits or more (one wave per split), else through LDS and its merge.  Keys outside a
+// segment's range are masked.  block = 512 (no tail waves: the tail keys are
+// added by k_split_tail).
+template <bool kPrep, bool kSplit>
 __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   uint16_t* sq = (uint16_t*)(lds + kLdsQ);
@@ -187,9 +202,9 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
 
   const int bx = blockIdx.x, xcd = bx & 7, yy = bx >> 3;
   int g, r;
-  if (a.R == 1) {
+  if (a.R == 1 || (kSplit && (a.R & 1))) {
     g = xcd;
-    r = 0;
+    r = yy;
   } else {
     g = 2 * (xcd & 3) + (yy & 1);
     r = (xcd >> 2) * (a.R >> 1) + (yy >> 1);
@@ -199,9 +214,15 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // Wave 8: a tail wave in range 0; in ranges 1..ne the extra wave, which
   // takes one group (an FP8 wave with a one-group buffer in the LDS the
   // others leave free).  The rest return.
-  const bool xw = w == kFpWaves && r != 0 && r <= a.ne;
-  if (w >= kFpWaves && r != 0 && !xw) return;
+  const bool xw = !kSplit && w == kFpWaves && r != 0 && r <= a.ne;
+  if (w >= kFpWaves && (kSplit || (r != 0 && !xw))) return;
   const float qscale = a.scale * kLog2e;
+  // split mode: this workgroup's splits [s0, s0 + ns)
+  int s0 = 0, ns = 0;
+  if constexpr (kSplit) {
+    s0 = (int)(((unsigned)r * (unsigned)a.nsplit) / (unsigned)a.R);
+    ns = (int)(((unsigned)(r + 1) * (unsigned)a.nsplit) / (unsigned)a.R) - s0;
+  }
 
   // ================================================================ FP8 waves
   if (w < kFpWaves || xw) {
@@ -218,6 +239,40 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       g0 = (int)(((unsigned)om * (unsigned)ngm) / (unsigned)nwv);
       g1 = (int)(((unsigned)(om + 1) * (unsigned)ngm) / (unsigned)nwv);
     }
+    // split mode: this wave's splits [sa, sb); with part_k > 1 it holds share
+    // part_i of its one split's groups (the split's waves are those w with
+    // w ns / 8 equal)
+    int sa = 0, sb = 0, part_i = 0, part_k = 1;
+    if constexpr (kSplit) {
+      if (ns <= kFpWaves) {
+        const int j = (w * ns) / kFpWaves;
+        const int fw = (j * kFpWaves + ns - 1) / ns, lw = ((j + 1) * kFpWaves + ns - 1) / ns;
+        sa = s0 + j;
+        sb = sa + 1;
+        part_k = lw - fw;
+        part_i = w - fw;
+      } else {
+        sa = s0 + (w * ns) / kFpWaves;
+        sb = s0 + ((w + 1) * ns) / kFpWaves;
+      }
+    }
+    // the committed keys [ka, kb) of split s that this wave takes (empty: ka == kb)
+    auto seg_keys = [&](int s, int& ka, int& kb) {
+      const int a0 = s * a.chunk;
+      const int b0 = min(min(a0 + a.chunk, a.total), a.committed);
+      ka = kb = 0;
+      if (a0 >= b0) return;
+      if (part_k > 1) {
+        const int G0 = a0 / G, ngr = (b0 + G - 1) / G - G0;
+        const int q0 = G0 + part_i * ngr / part_k, q1 = G0 + (part_i + 1) * ngr / part_k;
+        ka = max(a0, q0 * G);
+        kb = min(b0, q1 * G);
+        if (ka >= kb) ka = kb = 0;
+      } else {
+        ka = a0;
+        kb = b0;
+      }
+    };
     // (w & 7: the compiler then sees that a wave's DMA targets stay inside
     // the tile and scale regions, and does not make reads of the q rows wait
     // for them.)  The extra wave has one tile each of K and V: its second
@@ -265,11 +320,13 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rks, (lds_void_t*)slot, 2, soff, so, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (lds_void_t*)(slot + kScaleB), 2, soff, so, 0, 0);
     };
-    auto issue = [&](int u, __amdgpu_buffer_rsrc_t rc, uint8_t* dst) {
+    // (gend: the end of the unit's group range; a second group past it is
+    // not the range's: its slot gets the first group again)
+    auto issue = [&](int u, int gend, __amdgpu_buffer_rsrc_t rc, uint8_t* dst) {
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         if (t == 1 && xw) break;  // (its one group)
-        const int grp = u + t < g1 ? u + t : u;  // past the range: refetch
+        const int grp = u + t < gend ? u + t : u;  // past the range: refetch
 #pragma unroll
         for (int j = 0; j < 4; j++)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -278,15 +335,28 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
     };
     // (a wave without units fetches unit 0 and ignores it)
-    const int uf = g0 < g1 ? g0 : 0;
+    int uf = g0 < g1 ? g0 : 0, ufe = g1;
+    if constexpr (kSplit) {
+      uf = 0;
+      ufe = 1;
+      for (int s2 = sa; s2 < sb; s2++) {
+        int ka2, kb2;
+        seg_keys(s2, ka2, kb2);
+        if (ka2 < kb2) {
+          uf = ka2 / G;
+          ufe = (kb2 + G - 1) / G;
+          break;
+        }
+      }
+    }
     // Each wave fetches a unit's V only once the unit's K has landed (its K
     // DMAs then hold no more slots, so the V DMAs rarely wait to issue), and
     // multiplies K while V streams in: the workgroup's K lands first and
     // only P V follows the last bytes.
     __builtin_amdgcn_sched_barrier(0);
     issue_scales(uf, sw);
-    issue(uf, rk, kw);
-    if (xw) issue(uf, rv, vw);  // (its one group: K and V at once)
+    issue(uf, ufe, rk, kw);
+    if (xw) issue(uf, ufe, rv, vw);  // (its one group: K and V at once)
     __builtin_amdgcn_sched_barrier(0);
     if (w < GQA) {
       // the q row landed once at most the unit's 10 scale and K DMAs remain
@@ -343,13 +413,24 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     // scales and K, fetch its V, S^T, then (kMore) the next unit's scales and
     // K once this unit's K is read; softmax; wait for V; P V.  No load sits
     // under a branch, so every wait is exact.
-    auto unit = [&](int u, int slot, auto more_tag) {
+    // the unit's group range end (ge), key range (split mode: [ka, kb)) and
+    // the next unit (un, its range end une) -- set before each call
+    int ge = g1, ka = 0, kb = 0, un = 0, une = g1;
+    const int koff = 4 * (n >> 2) + c;  // key of output element v: 16 v + koff of the tile
+    // kVPre: the unit's V went out already (after the previous unit's P V,
+    // as its last 8 DMAs): wait for the scales and K only
+    auto unit = [&](int u, int slot, auto more_tag, auto vpre_tag) {
       constexpr bool kMore = decltype(more_tag)::value;
-      const bool t1ok = u + 1 < g1;
+      constexpr bool kVPre = decltype(vpre_tag)::value;
+      const bool t1ok = u + 1 < ge;
       // ---- S^T = K Q^T once the scales and K landed; V goes out now
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      __builtin_amdgcn_sched_barrier(0);
-      if (!xw) issue(u, rv, vw);
+      if constexpr (kVPre) {
+        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): all but this unit's V
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_sched_barrier(0);
+        if (!xw) issue(u, ge, rv, vw);
+      }
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t* scl = (const uint32_t*)(sw + slot * 2 * kScaleB);
       const int sh = scale_shift(u);  // (then group u + 1 is masked)
@@ -372,8 +453,8 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         // unit's may overwrite them
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_sched_barrier(0);
-        issue_scales(u + 2, sw + (slot ^ 1) * 2 * kScaleB);
-        issue(u + 2, rk, kw);
+        issue_scales(un, sw + (slot ^ 1) * 2 * kScaleB);
+        issue(un, une, rk, kw);
         __builtin_amdgcn_sched_barrier(0);
       }
       // ---- online softmax over the unit's 128 keys (4 per lane and tile)
@@ -384,6 +465,10 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         for (int v = 0; v < 4; v++) {
           S[t][v] *= t ? ks1 : ks0;
           if (t == 1 && !t1ok) S[t][v] = -1e30f;
+          if constexpr (kSplit) {
+            const int key = (u + t) * G + 16 * v + koff;
+            if (key < ka || key >= kb) S[t][v] = -1e30f;
+          }
           rmx = __builtin_fmaxf(rmx, S[t][v]);
         }
       rmx = head_max(rmx);
@@ -429,7 +514,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         T[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw3[0], raw3[1]), T[3], 0, 0, 0);
       }
       if constexpr (kMore) {
-        // this unit's V fully read before the next unit's V overwrites it
+        // this unit's V fully read: the caller sends the next unit's V
         __builtin_amdgcn_s_waitcnt(0xC07F);
       }
 #pragma unroll
@@ -438,24 +523,131 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         for (int v = 0; v < 4; v++) O[d][v] = __builtin_fmaf(O[d][v], oc[v], T[d][v]);
     };
     int slot = 0;
-    int u = g0;
-    for (; u + 2 < g1; u += 2, slot ^= 1) unit(u, slot, std::integral_constant<bool, true>{});
-    if (u < g1) unit(u, slot, std::integral_constant<bool, false>{});
+    if constexpr (!kSplit) {
+      using T_ = std::integral_constant<bool, true>;
+      using F_ = std::integral_constant<bool, false>;
+      int u = g0;
+      if (u + 2 < g1) {
+        // the first unit, then each next one with its V sent once the
+        // previous unit's P V has read the V buffer
+        un = u + 2;
+        unit(u, slot, T_{}, F_{});
+        issue(un, g1, rv, vw);
+        for (u += 2, slot ^= 1; u + 2 < g1; u += 2, slot ^= 1) {
+          un = u + 2;
+          unit(u, slot, T_{}, T_{});
+          issue(un, g1, rv, vw);
+        }
+        unit(u, slot, F_{}, T_{});
+      } else if (u < g1) {
+        unit(u, slot, F_{}, F_{});
+      }
+    } else {
+      // a finished split (or share): its (m, l, o) per head, then a fresh state
+      auto flush = [&](int sp) {
+        f32x4 Oc[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) Oc[d][v] = col4_sum(O[d][v]);
+        if (ns >= kFpWaves) {  // (then every split has one wave; else all go through the merge)
+          if (l < 16) {
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+              for (int v = 0; v < 4; v++)
+                a.po[((size_t)(g * GQA + v) * a.nsplit + sp) * D + 16 * d + l] = Oc[d][v];
+          }
+          if (l < GQA) {
+            a.pm[(g * GQA + l) * a.nsplit + sp] = lsum > 0.f ? mx * kLn2 : -1e30f;
+            a.pl[(g * GQA + l) * a.nsplit + sp] = lsum;
+          }
+        } else {
+          if (l < 16) {
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+              for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = Oc[d][v];
+          }
+          if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
+        }
+        mx = -1e30f;
+        lsum = 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; d++) O[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+      };
+      int sp = sa;
+      bool vpre = false;  // the current unit's V already sent
+      if (sp < sb) seg_keys(sp, ka, kb);
+      ge = (kb + G - 1) / G;
+      int u = ka < kb ? ka / G : -1;
+      while (sp < sb) {
+        if (u >= 0) {
+          // the next unit: in this split, else the first of a later split with keys
+          un = -1;
+          if (u + 2 < ge) {
+            un = u + 2;
+            une = ge;
+          } else {
+            for (int s2 = sp + 1; s2 < sb; s2++) {
+              int ka2, kb2;
+              seg_keys(s2, ka2, kb2);
+              if (ka2 < kb2) {
+                un = ka2 / G;
+                une = (kb2 + G - 1) / G;
+                break;
+              }
+            }
+          }
+          using T_ = std::integral_constant<bool, true>;
+          using F_ = std::integral_constant<bool, false>;
+          if (un >= 0) {
+            if (vpre) unit(u, slot, T_{}, T_{});
+            else unit(u, slot, T_{}, F_{});
+          } else {
+            if (vpre) unit(u, slot, F_{}, T_{});
+            else unit(u, slot, F_{}, F_{});
+          }
+          slot ^= 1;
+          if (u + 2 < ge) {
+            // the next unit's V, once this unit's P V has read the buffer
+            issue(un, une, rv, vw);
+            vpre = true;
+            u += 2;
+            continue;
+          }
+        }
+        flush(sp);
+        if (++sp >= sb) break;
+        seg_keys(sp, ka, kb);
+        ge = (kb + G - 1) / G;
+        u = ka < kb ? ka / G : -1;
+        // the next split's first unit's V (after the flush's stores, so that
+        // V stays the last 8 DMAs the unit start may leave outstanding)
+        vpre = false;
+        if (u >= 0 && un >= 0) {
+          issue(un, une, rv, vw);
+          vpre = true;
+        }
+      }
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (a wave without units: its fetch done)
-    // ---- the four key blocks of each (head, dim) summed; lanes 0..15 hold
-    // O[head v][16 delta + n]
-#pragma unroll
-    for (int d = 0; d < 4; d++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) O[d][v] = col4_sum(O[d][v]);
-    if (l < 16) {
+    if constexpr (!kSplit) {
+      // ---- the four key blocks of each (head, dim) summed; lanes 0..15 hold
+      // O[head v][16 delta + n]
 #pragma unroll
       for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = O[d][v];
+        for (int v = 0; v < 4; v++) O[d][v] = col4_sum(O[d][v]);
+      if (l < 16) {
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = O[d][v];
+      }
+      if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
     }
-    if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
-  } else {
+  } else if constexpr (!kSplit) {
     // ============================================================ tail waves
     const int i = w - kFpWaves;  // query head 4g + i
     const int tt = a.qpos + 1 - a.committed;  // tail keys (the fresh token last)
@@ -588,6 +780,31 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
 
   // ================================================================ merge
   if (w >= kFpWaves) return;  // (tail waves: their partial is in LDS)
+  if constexpr (kSplit) {
+    // splits shared by several waves (at most 7 splits here): merge the
+    // shares of each, head i = tid / 64, dim d
+    if (ns < kFpWaves && tid < GQA * D) {
+      const int i = tid >> 6, d = tid & 63, h = g * GQA + i;
+      for (int j = 0; j < ns; j++) {
+        const int fw = (j * kFpWaves + ns - 1) / ns, lw = ((j + 1) * kFpWaves + ns - 1) / ns;
+        float M = -1e30f;
+        for (int p = fw; p < lw; p++) M = __builtin_fmaxf(M, sml[p * GQA + i][0]);
+        float L = 0.f, Oacc = 0.f;
+        for (int p = fw; p < lw; p++) {
+          const float wt = __builtin_amdgcn_exp2f(sml[p * GQA + i][0] - M);
+          L = __builtin_fmaf(sml[p * GQA + i][1], wt, L);
+          Oacc = __builtin_fmaf(sO[(p * GQA + i) * D + d], wt, Oacc);
+        }
+        const int sp = s0 + j;
+        a.po[((size_t)h * a.nsplit + sp) * D + d] = Oacc;
+        if (d == 0) {
+          a.pm[h * a.nsplit + sp] = L > 0.f ? M * kLn2 : -1e30f;
+          a.pl[h * a.nsplit + sp] = L;
+        }
+      }
+    }
+    return;
+  }
   const int R = a.R;
   float* pg = a.part + (size_t)g * kMaxRanges * kPartF;  // kv head g's partials
   if (tid < GQA * D) {
@@ -676,6 +893,62 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   }
 }
 
+// The fp16 tail keys (committed..qpos) of the splits they fall in, merged
+// into the partials k_decode<false, true> wrote for those splits (the
+// reference's split kernel reads them with the committed keys,
+// engine.cu:417-444).  grid = 8 kv heads, block = 256: wave i takes query head
+// 4g + i, lane = tail key for the scores (fp32 from the fp16 rows), lane =
+// dim for o.
+__global__ __launch_bounds__(256) void k_split_tail(const uint16_t* __restrict__ q,
+                                                    const uint16_t* __restrict__ ktail,
+                                                    const uint16_t* __restrict__ vtail,
+                                                    int committed, int total, float scale,
+                                                    float* __restrict__ pm, float* __restrict__ pl,
+                                                    float* __restrict__ po, int nsplit, int chunk) {
+  const int g = blockIdx.x, i = threadIdx.x >> 6, l = threadIdx.x & 63, h = g * GQA + i;
+  const int tt = total - committed;
+  float sc = -1e30f;
+  if (l < tt) {
+    const uint16_t* kp = ktail + ((size_t)l * NKV + g) * D;
+    const uint16_t* qp = q + (size_t)h * D;
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d < D; d += 8) {
+      const u32x4 kk = *(const u32x4*)(kp + d), qq = *(const u32x4*)(qp + d);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        acc = __builtin_fmaf(h2f((uint16_t)qq[e]), h2f((uint16_t)kk[e]), acc);
+        acc = __builtin_fmaf(h2f((uint16_t)(qq[e] >> 16)), h2f((uint16_t)(kk[e] >> 16)), acc);
+      }
+    }
+    sc = acc * scale;
+  }
+  const int sfirst = committed / chunk, slast = (total - 1) / chunk;
+  for (int sp = sfirst; sp <= slast; sp++) {
+    // this split's tail keys, as tail rows [k0, k1)
+    const int k0 = max(committed, sp * chunk) - committed;
+    const int k1 = min(total, (sp + 1) * chunk) - committed;
+    const bool in = l >= k0 && l < k1;
+    const float mt = wave_max(in ? sc : -1e30f);
+    const float p = in ? fast_exp(sc - mt) : 0.f;
+    const float lt = wave_sum(p);
+    float ot = 0.f;
+    for (int k = k0; k < k1; k++) {
+      const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
+      ot = __builtin_fmaf(pk, h2f(vtail[((size_t)k * NKV + g) * D + l]), ot);
+    }
+    const size_t pi = (size_t)h * nsplit + sp;
+    const float m0 = pm[pi], l0 = pl[pi];
+    const float M = __builtin_fmaxf(m0, mt);
+    const float w0 = l0 > 0.f ? fast_exp(m0 - M) : 0.f, w1 = fast_exp(mt - M);
+    po[pi * D + l] = __builtin_fmaf(po[pi * D + l], w0, ot * w1);
+    if (l == 0) {
+      pm[pi] = M;
+      pl[pi] = __builtin_fmaf(l0, w0, lt * w1);
+    }
+  }
+}
+
 }  // namespace cia
 
 using namespace cia;
@@ -733,9 +1006,9 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
   if (da.prep.qw)
-    hipLaunchKernelGGL(k_decode<true>, dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+    hipLaunchKernelGGL((k_decode<true, false>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
   else
-    hipLaunchKernelGGL(k_decode<false>, dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+    hipLaunchKernelGGL((k_decode<false, false>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
   int st = launch_status();
   if (st) return st;
   if (mid_event) {
@@ -814,4 +1087,44 @@ extern "C" int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, co
   return cia_decode_mfma(q, kc8, vc8, ksc, vsc, (uint16_t*)ktail, (uint16_t*)vtail, nullptr,
                          nullptr, committed, qpos, scale, out, ws, kWsBytes, stream, nullptr,
                          nullptr);
+}
+
+// The reference's split partials on the matrix cores (no workspace: every
+// split is finished inside one workgroup): k_decode<false, true> over the
+// committed keys, then k_split_tail for the tail keys.  Internal entry of
+// cia_attn_decode_split for nsplit <= kSplitMfmaMax (arguments checked there).
+extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
+    const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+    const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed, int qpos,
+    float scale, float* pm, float* pl, float* po, int nsplit, void* stream) {
+  const int total = qpos + 1, chunk = (total + nsplit - 1) / nsplit;
+  int R = nsplit < kMaxRanges ? nsplit : kMaxRanges;
+  const int cus = device_cus();
+  if (cus > 0 && cus / NKV < R) R = cus / NKV > 0 ? cus / NKV : 1;
+  DecArgs da{};
+  da.q = q;
+  da.kc8 = (uint8_t*)kc8;
+  da.vc8 = (uint8_t*)vc8;
+  da.ksc = (uint16_t*)ksc;
+  da.vsc = (uint16_t*)vsc;
+  da.ktail = (uint16_t*)ktail;
+  da.vtail = (uint16_t*)vtail;
+  da.committed = committed;
+  da.qpos = qpos;
+  da.scale = scale;
+  da.ng = committed / G;
+  da.R = R;
+  da.pm = pm;
+  da.pl = pl;
+  da.po = po;
+  da.nsplit = nsplit;
+  da.chunk = chunk;
+  da.total = total;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL((k_decode<false, true>), dim3(NKV * R), dim3(64 * kFpWaves), 0, s, da);
+  int st = launch_status();
+  if (st || committed >= total) return st;
+  hipLaunchKernelGGL(k_split_tail, dim3(NKV), dim3(256), 0, s, q, ktail, vtail, committed, total,
+                     scale, pm, pl, po, nsplit, chunk);
+  return launch_status();
 }

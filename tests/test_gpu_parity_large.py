@@ -165,6 +165,30 @@ def test_decode_loop_32k_two_layers_through_commit(orc, cia, dev, producers):
         assert np.array_equal(_u16(L.vtail).reshape(64, -1)[:nt], refs[l].vtail.reshape(64, -1)[:nt])
 
 
+def _check_partials(pm, pl, po, rpm, rpl, rpo):
+    """A split's partial against the oracle's: empty splits exactly (m = -1e30,
+    l = 0, o = 0); else m within 1e-4 (the largest scaled score), l within
+    2e-4 relative, and the split's own attention output o / l within the
+    output tolerance 2e-3 + 1e-3 |ref|.  (o itself is a sum over up to 8192
+    keys whose terms cancel per dim; the matrix-core path rounds the softmax
+    numerators to fp16, so o is compared through o / l, the quantity the
+    combine uses.)"""
+    gpm, gpl = pm.cpu().numpy(), pl.cpu().numpy()
+    gpo = po.cpu().numpy().reshape(rpo.shape)
+    empty = rpl == 0
+    assert np.array_equal(gpl == 0, empty)
+    assert np.all(gpm[empty] == np.float32(-1e30)) and np.all(gpo[empty] == 0)
+    full = ~empty
+    np.testing.assert_allclose(gpm[full], rpm[full], rtol=0, atol=1e-4)
+    np.testing.assert_allclose(gpl[full], rpl[full], rtol=2e-4)
+    got = gpo[full] / gpl[full][:, None]
+    want = rpo[full] / rpl[full][:, None]
+    err = np.abs(got - want)
+    bad = err > 2e-3 + 1e-3 * np.abs(want)
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} split outputs o / l outside tolerance; "
+                           f"max abs err {err.max():.3g}")
+
+
 @pytest.fixture(scope="module")
 def cache131k(orc, dev):
     from cuda_inf_amd.layer import AttnLayer
@@ -197,9 +221,7 @@ def test_split_combine_131k(orc, cia, dev, cache131k, nsplit):
     torch.cuda.synchronize()
     _, r32, (rpm, rpl, rpo) = orc.attn_decode(_u16(q), ref, qpos, nsplit=nsplit, nthreads=8)
     assert_close_f16(_u16(out), r32)
-    np.testing.assert_allclose(pm.cpu().numpy(), rpm, rtol=0, atol=1e-4)
-    np.testing.assert_allclose(pl.cpu().numpy(), rpl, rtol=2e-4)
-    np.testing.assert_allclose(po.cpu().numpy().reshape(rpo.shape), rpo, rtol=2e-3, atol=2e-3)
+    _check_partials(pm, pl, po, rpm, rpl, rpo)
 
 
 def test_append_4096_bit_exact(orc, cia, dev):
@@ -218,3 +240,37 @@ def test_append_4096_bit_exact(orc, cia, dev):
     assert np.array_equal(_u16(L.vsc), ref.vsc)
     assert np.array_equal(_u16(L.ktail), ref.ktail)
     assert np.array_equal(_u16(L.vtail), ref.vtail)
+
+
+@pytest.mark.parametrize("ntok,nsplit", [(10109, 76), (25700, 200), (70000, 300), (2032, 7),
+                                         (5000, 3), (4300, 33), (200, 1), (3000, 1), (4096, 16),
+                                         (2032, 40), (777, 512), (64, 16), (131, 300), (1, 1)])
+def test_split_partials_geometry(orc, cia, dev, ntok, nsplit):
+    """Split geometries.  Matrix-core path (splits of 128 keys or more): the
+    tail straddling two splits (10109 / 76, 25700 / 200, and 70000 / 300 with
+    more than 8 splits per workgroup), odd workgroups per kv head (7, 3, 33),
+    one workgroup per kv head (nsplit 1), no tail (4096).  Splits of fewer
+    keys take the fp32 kernel: 2032 / 40, 777 / 512 and 131 / 300 (few keys,
+    empty splits), 64 / 16, and no committed group (1).  Every partial against
+    the oracle's, empty splits exactly (-1e30, 0, 0)."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    L = AttnLayer(ntok + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(ntok + 64)
+    _, k, v = qkv(ntok, seed=ntok + nsplit, device="cpu", outliers=True)
+    _append(L, k, v, 0, dev)
+    ref.append(_u16(k), _u16(v), 0)
+    qpos = ntok - 1
+    q, _, _ = qkv(1, seed=3 * nsplit, device="cpu", past=qpos)
+    pm = torch.full((32 * nsplit,), 7.0, device=dev)  # (stale values must all be replaced)
+    pl = torch.full((32 * nsplit,), 7.0, device=dev)
+    po = torch.full((32 * nsplit * 64,), 7.0, device=dev)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    K.attn_decode_split(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed,
+                        qpos, 0.125, pm, pl, po, nsplit)
+    K.attn_decode_combine(pm, pl, po, out, nsplit)
+    torch.cuda.synchronize()
+    _, r32, (rpm, rpl, rpo) = orc.attn_decode(_u16(q), ref, qpos, nsplit=nsplit, nthreads=8)
+    _check_partials(pm, pl, po, rpm, rpl, rpo)
+    assert_close_f16(_u16(out), r32)
