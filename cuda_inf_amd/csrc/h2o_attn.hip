@@ -11,8 +11,10 @@
 //          with k(t)[d] = e4m3(byte d) * fp32(scale of slot t)
 //   m    = max s over eligible slots (slot_pos[t] <= qpos, t < n_live)
 //   e(t) = exp_det(s(t) - m), 0 for ineligible slots
-//   l    = lane j of a wave sums e(j), e(j+64), ... in order, then the
-//          butterfly v = v + v[lane ^ off], off = 32..1
+//   l    = for each 64-slot block b ascending: lane j of a wave holds
+//          e(64b + j) (0 past the end), the butterfly v = v + v[lane ^ off],
+//          off = 32..1, gives the block's total; the totals are added in
+//          ascending b from 0
 //   p(t) = e(t) * (1/l)
 //   attn_sum[t] += p(t), one add per (query, head), queries then heads
 //                  ascending -- one of the orders the reference's atomics
@@ -29,10 +31,12 @@
 //                 the output, with fast exp -- the output is held to a
 //                 tolerance, not to bits.
 //   k_h2o_exp     same grid: m from the partial maxima (an exact max), e(t)
-//                 over s(t) in place; the first block of every head merges
-//                 the partials into the output row.
-//   k_h2o_mass    1024 slots per block: l and 1/l of every (query, head),
-//                 then attn_sum[t] += p(t) in the rule's order.
+//                 over s(t) in place and the block's total of the rule's l;
+//                 the first block of every head merges the partials into
+//                 the output row.
+//   k_h2o_mass    1024 slots per block: l (the block totals in order) and
+//                 1/l of every (query, head), then attn_sum[t] += p(t) in
+//                 the rule's order.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -57,6 +61,7 @@ struct H2oArgs {
   float* sc;       // [Sq][32][nblk * 64]: s(t), then e(t)
   float* part_o;   // [Sq][32][nblk][64]
   float* part_ml;  // [Sq][32][nblk][2]: block max, block sum
+  float* part_l;   // [Sq][32][nblk]: the block's total of the rule's l
   int n_live, nblk, qpos0, Sq;
   float scale;
   // single-token step that evicted a slot (placement in the scores launch):
@@ -265,7 +270,10 @@ __global__ __launch_bounds__(256) void k_h2o_exp(H2oArgs a) {
   float m = kNegInf;
   for (int b = lane; b < a.nblk; b += 64) m = __builtin_fmaxf(m, a.part_ml[(ph + b) * 2]);
   m = wave_max_fast(m);  // the exact maximum of s over eligible slots
-  *scp = (live && sp <= qpos) ? exp_det(sv - m) : 0.0f;
+  const float e = (live && sp <= qpos) ? exp_det(sv - m) : 0.0f;
+  *scp = e;
+  const float etot = wave_sum(e);  // the rule's butterfly over this block
+  if (lane == 0) a.part_l[ph + blk] = etot;
   if (blk != 0) return;
   // output row of head h: merge the blocks' partial softmaxes.  Lane b
   // weighs block b; lane d then sums the weighted partial rows.
@@ -296,13 +304,12 @@ __global__ __launch_bounds__(256) void k_h2o_exp(H2oArgs a) {
 }
 
 // grid = ceil(n_live / 1024), block = 1024: every block derives 1/l of
-// every (query, head) of the chunk (the same bits), then owns 1024 slots.
-// Loads are batched ahead of the in-order sums: a wave's two (query, head)
-// rows pr and pr + 16 load together, and the first query's numerators of
-// the thread's slot are loaded before the normalisers are summed.
+// every (query, head) of the chunk (the same bits) from the block totals,
+// then owns 1024 slots.  The first query's numerators of the thread's slot
+// are loaded before the totals are summed.
 __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
   __shared__ float inv[kChunk * NH];
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int tid = threadIdx.x;
   const size_t cp = (size_t)a.nblk * 64;
   const int t = blockIdx.x * 1024 + tid;
   const int tc = t < a.n_live ? t : 0;  // (slot 0 exists whenever a block runs)
@@ -310,35 +317,20 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
 #pragma unroll
   for (int h = 0; h < NH; h++) ev0[h] = a.sc[(size_t)h * cp + tc];
   const int npr = a.Sq * NH;
-  for (int pr = w; pr < npr; pr += 32) {
-    // rows pr and pr + 16 (the second one only when it exists; its loads
-    // then read row pr again and its sum is discarded)
-    const bool two = pr + 16 < npr;
-    const float* e0 = a.sc + pr * cp;
-    const float* e1 = a.sc + (two ? pr + 16 : pr) * cp;
-    float acc0 = 0.0f, acc1 = 0.0f;
-    // 2048 slots per round, all loads of a lane issued before its adds
-    // (slots past n_live add +0, which leaves the sum's bits unchanged: the
-    // numerators are never -0)
-    for (int t0 = 0; t0 < a.n_live; t0 += 64 * 32) {
-      float v0[32], v1[32];
+  if (tid < npr) {
+    // thread pr: the totals of row pr in ascending block order, 16 loads in
+    // flight at a time
+    const float* pt = a.part_l + (size_t)tid * a.nblk;
+    float l = 0.0f;
+    for (int b0 = 0; b0 < a.nblk; b0 += 16) {
+      float v[16];
 #pragma unroll
-      for (int u = 0; u < 32; u++) {
-        const int tt = t0 + lane + 64 * u;
-        v0[u] = tt < a.n_live ? e0[tt] : 0.0f;
-        v1[u] = tt < a.n_live ? e1[tt] : 0.0f;
-      }
+      for (int u = 0; u < 16; u++) v[u] = b0 + u < a.nblk ? pt[b0 + u] : 0.0f;
 #pragma unroll
-      for (int u = 0; u < 32; u++) acc0 = acc0 + v0[u];
-#pragma unroll
-      for (int u = 0; u < 32; u++) acc1 = acc1 + v1[u];
+      for (int u = 0; u < 16; u++)
+        if (b0 + u < a.nblk) l = l + v[u];
     }
-    const float l0 = wave_sum(acc0);  // the butterfly of the rule
-    const float l1 = wave_sum(acc1);
-    if (lane == 0) {
-      inv[pr] = 1.0f / l0;
-      if (two) inv[pr + 16] = 1.0f / l1;
-    }
+    inv[tid] = 1.0f / l;
   }
   __syncthreads();
   if (t >= a.n_live) return;
@@ -363,7 +355,7 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
 
 int64_t h2o_ws_bytes(int S, int C) {
   const int64_t sq = std::min(S, kChunk), nblk = (C + 63) / 64;
-  return sq * NH * (2 * nblk * 64 + 2 * nblk) * (int64_t)sizeof(float);
+  return sq * NH * (2 * nblk * 64 + 3 * nblk) * (int64_t)sizeof(float);
 }
 
 }  // namespace cia
@@ -403,6 +395,7 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     a.sc = (float*)ws;
     a.part_o = a.sc + (size_t)sq * NH * nblk * 64;
     a.part_ml = a.part_o + (size_t)sq * NH * nblk * 64;
+    a.part_l = a.part_ml + (size_t)sq * NH * nblk * 2;
     a.n_live = n_live;
     a.nblk = nblk;
     a.qpos0 = past + c0;
@@ -456,6 +449,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
   a.sc = (float*)ws;
   a.part_o = a.sc + (size_t)NH * nblk * 64;
   a.part_ml = a.part_o + (size_t)NH * nblk * 64;
+  a.part_l = a.part_ml + (size_t)NH * nblk * 2;
   a.n_live = n1;
   a.nblk = nblk;
   a.qpos0 = past;

@@ -10,8 +10,10 @@
 //   s(t) = fma chain over d = 0..63 of q[d]*k(t)[d] from 0, times scale
 //   m    = max s over eligible keys
 //   e(t) = exp_det(s(t) - m)          (0 for ineligible keys)
-//   l    = lane j of a wave sums e(j), e(j+64), ... in order, then the
-//          butterfly v = v + v[lane ^ off], off = 32..1
+//   l    = for each 64-key block b ascending: lane j of a wave holds
+//          e(64b + j) (0 past the end), the butterfly v = v + v[lane ^ off],
+//          off = 32..1, gives the block's total; the totals are added in
+//          ascending b from 0
 //   p(t) = e(t) * (1/l)
 //   attn_sum[t] += p(t), one add per (query, head), queries then heads
 //                  ascending -- one of the orders the reference's atomics
@@ -103,14 +105,17 @@ __global__ __launch_bounds__(256) void k_mass_stats(const uint16_t* __restrict__
     mx = __builtin_fmaxf(mx, dot_chain(qr, kx) * scale);
   }
   mx = wave_max(mx);
-  float acc = 0.0f;
-  for (int t = lane; t < n; t += 64) {
-    if (!src.ok(t, qpos)) continue;  // e = 0 adds nothing
-    float kx[D];
-    src.key(t, kvh, kx);
-    acc = acc + exp_det(dot_chain(qr, kx) * scale - mx);
+  float l = 0.0f;
+  for (int t0 = 0; t0 < n; t0 += 64) {
+    const int t = t0 + lane;
+    float e = 0.0f;
+    if (t < n && src.ok(t, qpos)) {
+      float kx[D];
+      src.key(t, kvh, kx);
+      e = exp_det(dot_chain(qr, kx) * scale - mx);
+    }
+    l = l + wave_sum(e);  // the block's butterfly, then the ordered total
   }
-  const float l = wave_sum(acc);  // the butterfly of the rule
   if (lane == 0) {
     stats[((size_t)i * NH + h) * 2] = mx;
     stats[((size_t)i * NH + h) * 2 + 1] = 1.0f / l;

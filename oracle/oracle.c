@@ -73,9 +73,11 @@
  *                then times `scale` (the 1/sqrt(64) softmax scale)
  *     m        = max of s(t) over eligible t
  *     e(t)     = exp_det(s(t) - m) for eligible t, else 0
- *     l        = tree64(e): lane j = 0..63 sums e(j), e(j+64), ... in
- *                ascending order from 0.0f, then six butterfly steps
- *                v[j] = v[j] + v[j ^ off] for off = 32,16,8,4,2,1
+ *     l        = blocked64(e): for each 64-slot block b ascending, the
+ *                block's 64 values v[j] = e(64b + j) (0 past the end)
+ *                reduced by six butterfly steps v[j] = v[j] + v[j ^ off]
+ *                for off = 32,16,8,4,2,1, and the block totals v[0] added
+ *                in ascending b from 0.0f
  *     p(t)     = e(t) * (1.0f / l)
  *   attn_sum[t] += p(t), one add per (i, h) in ascending i then ascending h.
  * The sum order is one of the orders the reference's atomics can produce.
@@ -406,20 +408,20 @@ ORC_HOT static void dot_chain_many(const float* q, const float* kT, int n,
   }
 }
 
-/* l = tree64 of e[0..n) as documented in the file header */
-static float tree64(const float* e, int n) {
-  float v[64];
-  for (int j = 0; j < 64; j++) {
-    float a = 0.0f;
-    for (int t = j; t < n; t += 64) a = a + e[t];
-    v[j] = a;
+/* l = blocked64 of e[0..n) as documented in the file header */
+static float blocked64(const float* e, int n) {
+  float l = 0.0f;
+  for (int b0 = 0; b0 < n; b0 += 64) {
+    float v[64];
+    for (int j = 0; j < 64; j++) v[j] = b0 + j < n ? e[b0 + j] : 0.0f;
+    for (int off = 32; off >= 1; off >>= 1) {
+      float w[64];
+      for (int j = 0; j < 64; j++) w[j] = v[j] + v[j ^ off];
+      memcpy(v, w, sizeof v);
+    }
+    l = l + v[0];
   }
-  for (int off = 32; off >= 1; off >>= 1) {
-    float w[64];
-    for (int j = 0; j < 64; j++) w[j] = v[j] + v[j ^ off];
-    memcpy(v, w, sizeof v);
-  }
-  return v[0];
+  return l;
 }
 
 /* the mass rule: given the scaled scores s[0..n) and an eligibility mask,
@@ -430,7 +432,7 @@ ORC_HOT static void mass_from_scores(const float* s, const unsigned char* ok,
   for (int t = 0; t < n; t++)
     if (ok[t] && s[t] > m) m = s[t];
   for (int t = 0; t < n; t++) e_scratch[t] = ok[t] ? orc_exp_det(s[t] - m) : 0.0f;
-  float l = tree64(e_scratch, n);
+  float l = blocked64(e_scratch, n);
   float inv = 1.0f / l;
   for (int t = 0; t < n; t++) p[t] = e_scratch[t] * inv;
 }
