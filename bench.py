@@ -624,8 +624,7 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
     window W, a P-token prompt, then `steps` single-token steps through the
     decode loop (slot choice on the device, no host round trip), timed as a
     whole; then 64 more steps with events around the scores launch (which
-    also chooses the slot and quantises the token) and the exp + mass
-    launches."""
+    also chooses the slot and quantises the token) and the mass launch."""
     import ctypes
     import torch
     from cuda_inf_amd import _lib, workload
@@ -669,12 +668,12 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
     res = {"slots": C, "window": W, "prompt": P, "steps": steps, "us_per_step": round(us, 2),
            "gbps": round(step_bytes / (us * 1e-6) / 1e9, 1),
            "scores_place_us_median": round(scores[extra // 2], 2),
-           "exp_mass_us_median": round(rest[extra // 2], 2),
+           "mass_us_median": round(rest[extra // 2], 2),
            "evictions": steps + extra + P - C,
-           "policy": "slot choice and quantisation inside the scores launch (3 launches per "
+           "policy": "slot choice and quantisation inside the scores launch (2 launches per "
                      "step, no host round trip)"}
     log(f"h2o C={C} W={W}: {us:.2f} us/step over {steps} steps; scores + placement "
-        f"{res['scores_place_us_median']} us, exp + mass {res['exp_mass_us_median']} us (medians)")
+        f"{res['scores_place_us_median']} us, mass {res['mass_us_median']} us (medians)")
     return res
 
 

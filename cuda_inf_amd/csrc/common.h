@@ -174,7 +174,9 @@ __device__ __forceinline__ float wave_sum_fast(float v) {
 // Sum over the wave in the tree order red[d] += red[d + s], s = 32, 16, ..,
 // 1 (the shared-memory reduction of engine.cu:153-154), every add "lower
 // lane + upper lane"; lanes d < s hold the tree's values at each level and
-// lane 0's total is broadcast.  No LDS traffic.
+// lane 0's total is broadcast.  No LDS traffic.  The same bits as wave_sum:
+// IEEE addition is commutative, so after each butterfly level lanes d and
+// d ^ off hold equal values, and lane 0's butterfly is this tree.
 __device__ __forceinline__ float wave_tree_sum(float v) {
   // (a row rotation by 16 - k hands lane i the value of lane i + k of its
   // 16-lane row for i < 16 - k)
@@ -188,7 +190,8 @@ __device__ __forceinline__ float wave_tree_sum(float v) {
 }
 
 // butterfly max / sum (xor 32, 16, ..., 1): the fixed order of the
-// deterministic attention mass
+// deterministic attention mass (wave_tree_sum gives the same sum without
+// LDS permutes)
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off));

@@ -9,34 +9,34 @@
 // machine (the CPU restatement follows the same rule):
 //   s(t) = fma chain over d = 0..63 of q[d]*k(t)[d] from 0, times scale,
 //          with k(t)[d] = e4m3(byte d) * fp32(scale of slot t)
-//   m    = max s over eligible slots (slot_pos[t] <= qpos, t < n_live)
-//   e(t) = exp_det(s(t) - m), 0 for ineligible slots
-//   l    = for each 64-slot block b ascending: lane j of a wave holds
-//          e(64b + j) (0 past the end), the butterfly v = v + v[lane ^ off],
-//          off = 32..1, gives the block's total; the totals are added in
-//          ascending b from 0
-//   p(t) = e(t) * (1/l)
+//   (slots in blocks b of 64: t = 64b + j)
+//   m_b  = max s over the eligible slots of block b (slot_pos[t] <= qpos,
+//          t < n_live), -inf if none;  m = max of the m_b
+//   e(t) = exp_det(s(t) - m_b), 0 for ineligible slots
+//   l_b  = lane j of a wave holds e(64b + j) (0 past the end), the
+//          butterfly v = v + v[lane ^ off], off = 32..1, gives l_b
+//   c_b  = exp_det(m_b - m), 0 for a block with no eligible slot
+//   l    = l_b * c_b added in ascending b from 0;  w_b = c_b * (1/l)
+//   p(t) = e(t) * w_b
 //   attn_sum[t] += p(t), one add per (query, head), queries then heads
 //                  ascending -- one of the orders the reference's atomics
 //                  can take.
 // Every product, sum and fma above is a single IEEE-rounded operation;
 // contraction is off in this file so the compiler adds no fusions.
 //
-// Three launches per chunk of up to kChunk queries, each spread over the
+// Two launches per chunk of up to kChunk queries, each spread over the
 // whole chip (the reference's one block of 32 threads per query scans the
 // buffer serially):
 //   k_h2o_scores  (64-slot block, kv head, query): one wave per query head
-//                 of the GQA group, lane = slot.  s(t) into scratch, and the
-//                 block's partial softmax (max, sum, V-weighted sum) for
-//                 the output, with fast exp -- the output is held to a
-//                 tolerance, not to bits.
-//   k_h2o_exp     same grid: m from the partial maxima (an exact max), e(t)
-//                 over s(t) in place and the block's total of the rule's l;
-//                 the first block of every head merges the partials into
-//                 the output row.
-//   k_h2o_mass    1024 slots per block: l (the block totals in order) and
-//                 1/l of every (query, head), then attn_sum[t] += p(t) in
-//                 the rule's order.
+//                 of the GQA group, lane = slot.  s(t), the block's maximum,
+//                 e(t) into scratch and the block's l_b; and the block's
+//                 partial softmax (max, sum, V-weighted sum) for the output,
+//                 with fast exp -- the output is held to a tolerance, not to
+//                 bits.
+//   k_h2o_mass    256-slot groups: m, l and the weights w_b of every
+//                 (query, head), attn_sum[t] += p(t) in the rule's order;
+//                 and, in workgroups of their own, the output rows merged
+//                 from the blocks' partials.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -58,10 +58,10 @@ struct H2oArgs {
   const int32_t* slot_pos;
   uint16_t* out;  // first output row of the chunk
   float* attn_sum;
-  float* sc;       // [Sq][32][nblk * 64]: s(t), then e(t)
+  float* sc;       // [Sq][32][nblk * 64]: e(t) = exp_det(s(t) - m_b)
   float* part_o;   // [Sq][32][nblk][64]
   float* part_ml;  // [Sq][32][nblk][2]: block max, block sum
-  float* part_l;   // [Sq][32][nblk]: the block's total of the rule's l
+  float* part_l;   // [Sq][32][nblk]: l_b, the block's butterfly total of e
   int n_live, nblk, qpos0, Sq;
   float scale;
   // single-token step that evicted a slot (placement in the scores launch):
@@ -235,9 +235,12 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
     }
     s = acc * a.scale;
   }
-  a.sc[((size_t)i * NH + h) * (a.nblk * 64) + t] = s;
-  // the block's partial softmax for the output
+  // the block's maximum m_b; the rule's numerators and l_b
   const float mb = wave_max_fast(s);
+  const float ed = ok ? exp_det(s - mb) : 0.0f;
+  a.sc[((size_t)i * NH + h) * (a.nblk * 64) + t] = ed;
+  const float lbd = wave_tree_sum(ed);  // the rule's butterfly total
+  // the block's partial softmax for the output
   const float e = ok ? fast_exp(s - mb) : 0.0f;
   const float lb = wave_sum_fast(e);
   const float wgt = ok ? e * h2f(vs16) : 0.0f;
@@ -254,103 +257,188 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   if (lane == 0) {
     a.part_ml[pi * 2] = mb;
     a.part_ml[pi * 2 + 1] = lb;
+    a.part_l[pi] = lbd;
   }
 }
 
-// grid = (nblk, 8, Sq), block = 256
-__global__ __launch_bounds__(256) void k_h2o_exp(H2oArgs a) {
-  const int blk = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
-  const int lane = threadIdx.x & 63, h = kvh * GQA + wave_id();
-  const int qpos = a.qpos0 + i, t = blk * 64 + lane;
-  const size_t ph = ((size_t)i * NH + h) * a.nblk;
-  const bool live = t < a.n_live;
-  const int sp = live ? a.slot_pos[t] : 0x7FFFFFFF;
-  float* scp = a.sc + ((size_t)i * NH + h) * (a.nblk * 64) + t;
-  const float sv = *scp;
-  float m = kNegInf;
-  for (int b = lane; b < a.nblk; b += 64) m = __builtin_fmaxf(m, a.part_ml[(ph + b) * 2]);
-  m = wave_max_fast(m);  // the exact maximum of s over eligible slots
-  const float e = (live && sp <= qpos) ? exp_det(sv - m) : 0.0f;
-  *scp = e;
-  const float etot = wave_sum(e);  // the rule's butterfly over this block
-  if (lane == 0) a.part_l[ph + blk] = etot;
-  if (blk != 0) return;
-  // output row of head h: merge the blocks' partial softmaxes.  Lane b
-  // weighs block b; lane d then sums the weighted partial rows.
-  float L = 0.0f, O = 0.0f;
-  for (int b0 = 0; b0 < a.nblk; b0 += 64) {
-    const int nb = min(64, a.nblk - b0);
-    float cb = 0.0f, lb = 0.0f;
-    if (lane < nb) {
-      const float mb = a.part_ml[(ph + b0 + lane) * 2];
-      lb = a.part_ml[(ph + b0 + lane) * 2 + 1];
-      cb = mb > kNegInf ? fast_exp(mb - m) : 0.0f;
+constexpr int kMassBlk = 4;         // 64-slot blocks per slot group (256 threads)
+constexpr int kMassMaxWg = 256;     // slot workgroups at most
+constexpr int kRowPass = 8;         // (query, head) rows per wave per pass
+
+// One output row of the chunk: the 64-slot blocks' partial softmaxes merged
+// (lane b weighs block b, lane d then sums dim d); 32 blocks' loads at a time.
+__device__ __forceinline__ void h2o_out_row(const H2oArgs& a, int pr, int lane) {
+  const size_t ph = (size_t)pr * a.nblk;
+  float m = kNegInf, L = 0.0f, O = 0.0f;
+  for (int c0 = 0; c0 < a.nblk; c0 += 32) {
+    const int nb = min(32, a.nblk - c0);
+    const bool in = lane < nb;
+    const float mb = in ? a.part_ml[(ph + c0 + lane) * 2] : kNegInf;
+    const float lb = in ? a.part_ml[(ph + c0 + lane) * 2 + 1] : 0.0f;
+    const float* po = a.part_o + (ph + c0) * D + lane;
+    float ov[32];
+#pragma unroll
+    for (int u = 0; u < 32; u++) ov[u] = u < nb ? po[u * D] : 0.0f;
+    const float mn = __builtin_fmaxf(m, wave_max_fast(mb));
+    if (mn == kNegInf) continue;
+    const float r = m == kNegInf ? 0.0f : fast_exp(m - mn);
+    const float cb = mb > kNegInf ? fast_exp(mb - mn) : 0.0f;
+    L = L * r + wave_sum_fast(cb * lb);
+    O = O * r;
+#pragma unroll
+    for (int u = 0; u < 32; u++) {
+      const float cj = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cb), u));
+      O = __builtin_fmaf(cj, ov[u], O);
     }
-    L += wave_sum_fast(cb * lb);
-    const float* po = a.part_o + (ph + b0) * D + lane;
-    for (int j = 0; j < nb; j += 16) {
-      float ov[16];
+    m = mn;
+  }
+  a.out[(size_t)pr * D + lane] = f2h(O / L);
+}
+
+// grid = nsw + ceil(Sq * 32 / 4), block = 256.  Workgroups below nsw are
+// slot workgroups: each takes m and 1/l of every (query, head) row of the
+// chunk (wave-parallel over the block maxima and totals; l in block order
+// through readlane), then owns the 256-slot groups g = blockIdx, blockIdx +
+// nsw, ..: the weights w_b of the group's 4 blocks, then attn_sum[t] +=
+// e(t) w_b in (query, head) order.  The rest merge the output rows, one per
+// wave, alongside.
+__global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
+  __shared__ float wsh[kChunk * NH * kMassBlk];  // w_b of the group's blocks
+  __shared__ float mi[kChunk * NH][2];           // m, 1/l per row
+  const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+  const int npr = a.Sq * NH;
+  if ((int)blockIdx.x >= nsw) {
+    const int pr = ((int)blockIdx.x - nsw) * 4 + wv;
+    if (pr < npr) h2o_out_row(a, pr, lane);
+    return;
+  }
+  const size_t cp = (size_t)a.nblk * 64;
+  const int ng = (a.n_live + 255) / 256;
+  const int placed = a.placed ? *a.placed : -1;  // the slot evicted by this step
+  int g = blockIdx.x;
+  int b0 = g * kMassBlk;
+  // a group's loads that do not wait for the weights: the numerators of the
+  // first query, the slot's position and mass
+  float ev0[NH], acc = 0.0f;
+  int sp = 0;
+  auto fetch = [&](int gg) {
+    const int t = gg * 256 + tid;
+    const int tc = t < a.n_live ? t : 0;
 #pragma unroll
-      for (int u = 0; u < 16; u++) ov[u] = j + u < nb ? po[(j + u) * D] : 0.0f;
+    for (int h = 0; h < NH; h++) ev0[h] = a.sc[(size_t)h * cp + tc];
+    sp = a.slot_pos[tc];
+    acc = a.attn_sum[tc];
+  };
+  fetch(g);
+  // ---- m and 1/l of every row (lane = block); the first group's w_b
+  if (a.nblk <= 64) {
+    const bool in = lane < a.nblk;
+    for (int r0 = wv; r0 < npr; r0 += 4 * kRowPass) {
+      float mbv[kRowPass], prod[kRowPass], cb[kRowPass], l[kRowPass];
 #pragma unroll
-      for (int u = 0; u < 16; u++) {
-        const float cj = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cb), j + u));
-        O = __builtin_fmaf(cj, ov[u], O);
+      for (int k = 0; k < kRowPass; k++) {
+        const int r = r0 + 4 * k;
+        const bool ok = in && r < npr;
+        mbv[k] = ok ? a.part_ml[((size_t)r * a.nblk + lane) * 2] : kNegInf;
+        prod[k] = ok ? a.part_l[(size_t)r * a.nblk + lane] : 0.0f;
+      }
+      float m[kRowPass];
+#pragma unroll
+      for (int k = 0; k < kRowPass; k++) {
+        m[k] = wave_max_fast(mbv[k]);
+        cb[k] = mbv[k] == kNegInf ? 0.0f : exp_det(mbv[k] - m[k]);
+        prod[k] = prod[k] * cb[k];
+        l[k] = 0.0f;
+      }
+      // l in block order, the rows' chains side by side
+      for (int b = 0; b < a.nblk; b++) {
+#pragma unroll
+        for (int k = 0; k < kRowPass; k++)
+          l[k] = l[k] + __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prod[k]), b));
+      }
+#pragma unroll
+      for (int k = 0; k < kRowPass; k++) {
+        const int r = r0 + 4 * k;
+        const float inv = 1.0f / l[k];
+        if (r < npr) {
+          if (lane == 0) {
+            mi[r][0] = m[k];
+            mi[r][1] = inv;
+          }
+          if (lane >= b0 && lane < b0 + kMassBlk) wsh[r * kMassBlk + (lane - b0)] = cb[k] * inv;
+        }
       }
     }
-  }
-  a.out[((size_t)i * NH + h) * D + lane] = f2h(O / L);
-}
-
-// grid = ceil(n_live / 1024), block = 1024: every block derives 1/l of
-// every (query, head) of the chunk (the same bits) from the block totals,
-// then owns 1024 slots.  The first query's numerators of the thread's slot
-// are loaded before the totals are summed.
-__global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a) {
-  __shared__ float inv[kChunk * NH];
-  const int tid = threadIdx.x;
-  const size_t cp = (size_t)a.nblk * 64;
-  const int t = blockIdx.x * 1024 + tid;
-  const int tc = t < a.n_live ? t : 0;  // (slot 0 exists whenever a block runs)
-  float ev0[NH];
-#pragma unroll
-  for (int h = 0; h < NH; h++) ev0[h] = a.sc[(size_t)h * cp + tc];
-  const int npr = a.Sq * NH;
-  if (tid < npr) {
-    // thread pr: the totals of row pr in ascending block order, 16 loads in
-    // flight at a time
-    const float* pt = a.part_l + (size_t)tid * a.nblk;
-    float l = 0.0f;
-    for (int b0 = 0; b0 < a.nblk; b0 += 16) {
-      float v[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = b0 + u < a.nblk ? pt[b0 + u] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 16; u++)
-        if (b0 + u < a.nblk) l = l + v[u];
+  } else {
+    for (int r = wv; r < npr; r += 4) {
+      const size_t rb = (size_t)r * a.nblk;
+      float m = kNegInf;
+      for (int c0 = 0; c0 < a.nblk; c0 += 64)
+        m = __builtin_fmaxf(m, c0 + lane < a.nblk ? a.part_ml[(rb + c0 + lane) * 2] : kNegInf);
+      m = wave_max_fast(m);
+      float l = 0.0f, cw = 0.0f;
+      for (int c0 = 0; c0 < a.nblk; c0 += 64) {
+        const int b = c0 + lane;
+        const float mb = b < a.nblk ? a.part_ml[(rb + b) * 2] : kNegInf;
+        const float lt = b < a.nblk ? a.part_l[rb + b] : 0.0f;
+        const float cb = mb == kNegInf ? 0.0f : exp_det(mb - m);
+        const float prod = lt * cb;
+        const int nb = min(64, a.nblk - c0);
+        for (int u = 0; u < nb; u++)
+          l = l + __builtin_bit_cast(
+                      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prod), u));
+        if (b >= b0 && b < b0 + kMassBlk) cw = cb;
+      }
+      const float inv = 1.0f / l;
+      if (lane == 0) {
+        mi[r][0] = m;
+        mi[r][1] = inv;
+      }
+      const int bl = (b0 & 63) + (lane & 3);  // lanes 0..3: the first group's blocks
+      const float cwl = __builtin_bit_cast(
+          float, __builtin_amdgcn_ds_bpermute(bl << 2, __builtin_bit_cast(int, cw)));
+      if (lane < kMassBlk) wsh[r * kMassBlk + lane] = cwl * inv;
     }
-    inv[tid] = 1.0f / l;
   }
   __syncthreads();
-  if (t >= a.n_live) return;
-  const bool re = a.placed && t == *a.placed;  // the slot evicted by this step
-  const int sp = re ? a.posj : a.slot_pos[t];
-  float acc = re ? 0.0f : a.attn_sum[t];
-  if (sp <= a.qpos0) {
+  for (;;) {
+    const int t = g * 256 + tid;
+    if (t < a.n_live) {
+      const int bl = (t >> 6) - b0;
+      const bool re = t == placed;
+      const int spt = re ? a.posj : sp;
+      float x = re ? 0.0f : acc;
+      if (spt <= a.qpos0) {
 #pragma unroll
-    for (int h = 0; h < NH; h++) acc = acc + ev0[h] * inv[h];
+        for (int h = 0; h < NH; h++) x = x + ev0[h] * wsh[h * kMassBlk + bl];
+      }
+      for (int i = 1; i < a.Sq; i++) {
+        if (spt > a.qpos0 + i) continue;
+        float ev[NH];
+#pragma unroll
+        for (int h = 0; h < NH; h++) ev[h] = a.sc[(size_t)(i * NH + h) * cp + t];
+#pragma unroll
+        for (int h = 0; h < NH; h++) x = x + ev[h] * wsh[(i * NH + h) * kMassBlk + bl];
+      }
+      a.attn_sum[t] = x;
+      if (re) a.slotpos_w[t] = a.posj;
+    }
+    g += nsw;
+    if (g >= ng) break;
+    // the next group: its loads, then its w_b
+    b0 = g * kMassBlk;
+    fetch(g);
+    __syncthreads();  // the previous group's weights are read
+    for (int x = tid; x < npr * kMassBlk; x += 256) {
+      const int r = x / kMassBlk, b = b0 + x % kMassBlk;
+      const float mb = b < a.nblk ? a.part_ml[((size_t)r * a.nblk + b) * 2] : kNegInf;
+      const float cb = mb == kNegInf ? 0.0f : exp_det(mb - mi[r][0]);
+      wsh[x] = cb * mi[r][1];
+    }
+    __syncthreads();
   }
-  for (int i = 1; i < a.Sq; i++) {
-    if (sp > a.qpos0 + i) continue;
-    float ev[NH];
-#pragma unroll
-    for (int h = 0; h < NH; h++) ev[h] = a.sc[(size_t)(i * NH + h) * cp + t];
-#pragma unroll
-    for (int h = 0; h < NH; h++) acc = acc + ev[h] * inv[i * NH + h];
-  }
-  a.attn_sum[t] = acc;
-  if (re) a.slotpos_w[t] = a.posj;
 }
 
 int64_t h2o_ws_bytes(int S, int C) {
@@ -407,16 +495,15 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     hipLaunchKernelGGL(k_h2o_scores<false>, dim3(nblk, NKV, sq), dim3(256), 0, s, a, H2oPlace{});
     int st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(k_h2o_exp, dim3(nblk, NKV, sq), dim3(256), 0, s, a);
-    if ((st = launch_status())) return st;
-    hipLaunchKernelGGL(k_h2o_mass, dim3((n_live + 1023) / 1024), dim3(1024), 0, s, a);
+    const int nsw = std::min((n_live + 255) / 256, kMassMaxWg);
+    hipLaunchKernelGGL(k_h2o_mass, dim3(nsw + (sq * NH + 3) / 4), dim3(256), 0, s, a, nsw);
     if ((st = launch_status())) return st;
   }
   return CIA_OK;
 }
 
-// One decode step of an H2O layer in three launches: the token placed and
-// quantised inside the scores launch (H2oPlace), then exp and mass.  The
+// One decode step of an H2O layer in two launches: the token placed and
+// quantised inside the scores launch (H2oPlace), then the mass launch.  The
 // same slots, positions, bytes and masses as cia_h2o_place followed by
 // cia_attention_h2o for S = 1.  mid_event (may be NULL) is recorded after
 // the scores launch.
@@ -469,13 +556,12 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
       return CIA_ERR_HIP;
     }
   }
-  hipLaunchKernelGGL(k_h2o_exp, dim3(nblk, NKV, 1), dim3(256), 0, s, a);
-  if ((st = launch_status())) return st;
   if (n0 >= C) {
     a.placed = dst_slots;
     a.slotpos_w = slot_pos;
   }
-  hipLaunchKernelGGL(k_h2o_mass, dim3((n1 + 1023) / 1024), dim3(1024), 0, s, a);
+  const int nsw = std::min((n1 + 255) / 256, kMassMaxWg);
+  hipLaunchKernelGGL(k_h2o_mass, dim3(nsw + NH / 4), dim3(256), 0, s, a, nsw);
   if ((st = launch_status())) return st;
   *n_live = n1;
   return CIA_OK;

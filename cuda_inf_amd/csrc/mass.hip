@@ -8,13 +8,14 @@
 // identical bits on any IEEE-754 machine (the CPU restatement follows the
 // same rule):
 //   s(t) = fma chain over d = 0..63 of q[d]*k(t)[d] from 0, times scale
-//   m    = max s over eligible keys
-//   e(t) = exp_det(s(t) - m)          (0 for ineligible keys)
-//   l    = for each 64-key block b ascending: lane j of a wave holds
-//          e(64b + j) (0 past the end), the butterfly v = v + v[lane ^ off],
-//          off = 32..1, gives the block's total; the totals are added in
-//          ascending b from 0
-//   p(t) = e(t) * (1/l)
+//   (keys in blocks b of 64: t = 64b + j)
+//   m_b  = max s over the eligible keys of block b;  m = max of the m_b
+//   e(t) = exp_det(s(t) - m_b)        (0 for ineligible keys)
+//   l_b  = lane j of a wave holds e(64b + j) (0 past the end), the
+//          butterfly v = v + v[lane ^ off], off = 32..1, gives l_b
+//   c_b  = exp_det(m_b - m), 0 for a block with no eligible key
+//   l    = l_b * c_b added in ascending b from 0
+//   p(t) = e(t) * (c_b * (1/l))
 //   attn_sum[t] += p(t), one add per (query, head), queries then heads
 //                  ascending -- one of the orders the reference's atomics
 //                  can take.
@@ -108,13 +109,17 @@ __global__ __launch_bounds__(256) void k_mass_stats(const uint16_t* __restrict__
   float l = 0.0f;
   for (int t0 = 0; t0 < n; t0 += 64) {
     const int t = t0 + lane;
-    float e = 0.0f;
-    if (t < n && src.ok(t, qpos)) {
+    const bool ok = t < n && src.ok(t, qpos);
+    float sv = -__builtin_inff();
+    if (ok) {
       float kx[D];
       src.key(t, kvh, kx);
-      e = exp_det(dot_chain(qr, kx) * scale - mx);
+      sv = dot_chain(qr, kx) * scale;
     }
-    l = l + wave_sum(e);  // the block's butterfly, then the ordered total
+    const float mb = wave_max_fast(sv);
+    const float e = ok ? exp_det(sv - mb) : 0.0f;
+    const float cb = mb == -__builtin_inff() ? 0.0f : exp_det(mb - mx);
+    l = l + wave_tree_sum(e) * cb;  // the block's butterfly, then the ordered total
   }
   if (lane == 0) {
     stats[((size_t)i * NH + h) * 2] = mx;
@@ -123,33 +128,38 @@ __global__ __launch_bounds__(256) void k_mass_stats(const uint16_t* __restrict__
 }
 
 // attn_sum[t] += p for every (query, head) in order.  grid = ceil(n/64),
-// block = 64; thread t owns key t.
+// block = 64: one wave per 64-key block, lane j owns key 64b + j; the wave
+// takes the block's maximum m_b itself, so every lane runs every reduction.
 template <class Src>
 __global__ __launch_bounds__(64) void k_mass_accum(const uint16_t* __restrict__ q, Src src, int S,
                                                    int past, float scale,
                                                    const float* __restrict__ stats,
                                                    float* __restrict__ attn_sum, int nkeys) {
-  const int t = blockIdx.x * 64 + threadIdx.x;
-  if (t >= nkeys) return;
-  float a = attn_sum[t];
+  const int t0 = blockIdx.x * 64, t = t0 + threadIdx.x;
+  const bool live = t < nkeys;
+  const int tc = live ? t : t0;  // (key t0 < nkeys exists in every block)
+  float a = live ? attn_sum[t] : 0.0f;
   for (int i = 0; i < S; i++) {
     const int qpos = past + i;
-    if (t >= src.count(qpos) || !src.ok(t, qpos)) continue;
+    if (t0 >= src.count(qpos)) continue;  // uniform: the block has no visible key
+    const bool ok = live && t < src.count(qpos) && src.ok(t, qpos);
     for (int kvh = 0; kvh < NKV; kvh++) {
       float kx[D];
-      src.key(t, kvh, kx);
+      src.key(tc, kvh, kx);
       for (int j = 0; j < GQA; j++) {
         const int h = kvh * GQA + j;
         float qr[D];
         load_q(q + ((size_t)i * NH + h) * D, qr);
         const float m = stats[((size_t)i * NH + h) * 2];
         const float inv = stats[((size_t)i * NH + h) * 2 + 1];
-        const float p = exp_det(dot_chain(qr, kx) * scale - m) * inv;
-        a = a + p;
+        const float sv = ok ? dot_chain(qr, kx) * scale : -__builtin_inff();
+        const float mb = wave_max_fast(sv);
+        const float w = exp_det(mb - m) * inv;  // mb is finite: key t0 is visible
+        if (ok) a = a + exp_det(sv - mb) * w;
       }
     }
   }
-  attn_sum[t] = a;
+  if (live) attn_sum[t] = a;
 }
 
 }  // namespace cia

@@ -71,14 +71,17 @@
  *     kd(t)[d] = e4m3(byte) * scale   (exact in fp32)  or the fp16 tail value
  *     s(t)     = fmaf-chain over d = 0..63 of q[d]*kd(t)[d], from 0.0f,
  *                then times `scale` (the 1/sqrt(64) softmax scale)
- *     m        = max of s(t) over eligible t
- *     e(t)     = exp_det(s(t) - m) for eligible t, else 0
- *     l        = blocked64(e): for each 64-slot block b ascending, the
- *                block's 64 values v[j] = e(64b + j) (0 past the end)
+ *     (the slots in blocks b of 64: slot t = 64b + j, j = 0..63)
+ *     m_b      = max of s(t) over the eligible t of block b (-inf if none)
+ *     m        = max of m_b over the blocks
+ *     e(t)     = exp_det(s(t) - m_b) for eligible t, else 0
+ *     l_b      = the block's 64 values v[j] = e(64b + j) (0 past the end)
  *                reduced by six butterfly steps v[j] = v[j] + v[j ^ off]
- *                for off = 32,16,8,4,2,1, and the block totals v[0] added
- *                in ascending b from 0.0f
- *     p(t)     = e(t) * (1.0f / l)
+ *                for off = 32,16,8,4,2,1; l_b = v[0]
+ *     c_b      = exp_det(m_b - m), 0 for a block with no eligible slot
+ *     l        = l_b * c_b added in ascending b from 0.0f
+ *     w_b      = c_b * (1.0f / l)
+ *     p(t)     = e(t) * w_b
  *   attn_sum[t] += p(t), one add per (i, h) in ascending i then ascending h.
  * The sum order is one of the orders the reference's atomics can produce.
  *
@@ -408,33 +411,42 @@ ORC_HOT static void dot_chain_many(const float* q, const float* kT, int n,
   }
 }
 
-/* l = blocked64 of e[0..n) as documented in the file header */
-static float blocked64(const float* e, int n) {
+/* the mass rule: given the scaled scores s[0..n) and an eligibility mask,
+ * write p[0..n) (file header: block maxima m_b, numerators against them,
+ * block totals by butterfly, weighted by exp_det(m_b - m) in block order). */
+ORC_HOT static void mass_from_scores(const float* s, const unsigned char* ok,
+                                     int n, float* e_scratch, float* p) {
+  const int nb = (n + 63) / 64;
+  float* mb = (float*)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1));
+  float* wb = (float*)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1));
+  float m = -INFINITY;
+  for (int b = 0; b < nb; b++) {
+    float x = -INFINITY;
+    for (int t = 64 * b; t < n && t < 64 * b + 64; t++)
+      if (ok[t] && s[t] > x) x = s[t];
+    for (int t = 64 * b; t < n && t < 64 * b + 64; t++)
+      e_scratch[t] = ok[t] ? orc_exp_det(s[t] - x) : 0.0f;
+    if (x > m) m = x;
+    mb[b] = x;
+  }
   float l = 0.0f;
-  for (int b0 = 0; b0 < n; b0 += 64) {
+  for (int b = 0; b < nb; b++) {
     float v[64];
-    for (int j = 0; j < 64; j++) v[j] = b0 + j < n ? e[b0 + j] : 0.0f;
+    for (int j = 0; j < 64; j++) v[j] = 64 * b + j < n ? e_scratch[64 * b + j] : 0.0f;
     for (int off = 32; off >= 1; off >>= 1) {
       float w[64];
       for (int j = 0; j < 64; j++) w[j] = v[j] + v[j ^ off];
       memcpy(v, w, sizeof v);
     }
-    l = l + v[0];
+    const float cb = mb[b] == -INFINITY ? 0.0f : orc_exp_det(mb[b] - m);
+    wb[b] = cb;
+    l = l + v[0] * cb;
   }
-  return l;
-}
-
-/* the mass rule: given the scaled scores s[0..n) and an eligibility mask,
- * write p[0..n). */
-ORC_HOT static void mass_from_scores(const float* s, const unsigned char* ok,
-                                     int n, float* e_scratch, float* p) {
-  float m = -INFINITY;
-  for (int t = 0; t < n; t++)
-    if (ok[t] && s[t] > m) m = s[t];
-  for (int t = 0; t < n; t++) e_scratch[t] = ok[t] ? orc_exp_det(s[t] - m) : 0.0f;
-  float l = blocked64(e_scratch, n);
-  float inv = 1.0f / l;
-  for (int t = 0; t < n; t++) p[t] = e_scratch[t] * inv;
+  const float inv = 1.0f / l;
+  for (int b = 0; b < nb; b++) wb[b] = wb[b] * inv;
+  for (int t = 0; t < n; t++) p[t] = e_scratch[t] * wb[t / 64];
+  free(mb);
+  free(wb);
 }
 
 /* ------------------------------------------------------------------ */
