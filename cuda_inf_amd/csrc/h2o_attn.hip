@@ -261,9 +261,10 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   }
 }
 
-constexpr int kMassBlk = 4;         // 64-slot blocks per slot group (256 threads)
+constexpr int kMassBlk = 4;         // 64-slot blocks per slot group (256 slots)
 constexpr int kMassMaxWg = 256;     // slot workgroups at most
-constexpr int kRowPass = 8;         // (query, head) rows per wave per pass
+constexpr int kMassWaves = 16;      // waves per mass workgroup
+constexpr int kPwStride = 68;       // floats per row of a wave's block products
 
 // One output row of the chunk: the 64-slot blocks' partial softmaxes merged
 // (lane b weighs block b, lane d then sums dim d); 32 blocks' loads at a time.
@@ -296,20 +297,23 @@ __device__ __forceinline__ void h2o_out_row(const H2oArgs& a, int pr, int lane) 
   a.out[(size_t)pr * D + lane] = f2h(O / L);
 }
 
-// grid = nsw + ceil(Sq * 32 / 4), block = 256.  Workgroups below nsw are
-// slot workgroups: each takes m and 1/l of every (query, head) row of the
-// chunk (wave-parallel over the block maxima and totals; l in block order
-// through readlane), then owns the 256-slot groups g = blockIdx, blockIdx +
-// nsw, ..: the weights w_b of the group's 4 blocks, then attn_sum[t] +=
-// e(t) w_b in (query, head) order.  The rest merge the output rows, one per
-// wave, alongside.
-__global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
+// grid = nsw + ceil(Sq * 32 / 16), block = 1024.  Workgroups below nsw are
+// slot workgroups: their 16 waves take m and 1/l of every (query, head) row
+// of the chunk, kRowPass rows per wave at a time (lane = block: the maxima
+// and c_b wave-parallel; then one lane per row adds the row's l_b c_b in
+// block order from LDS).  The first 256 threads then own the 256-slot
+// groups g = blockIdx, blockIdx + nsw, ..: the weights w_b of the group's 4
+// blocks, then attn_sum[t] += e(t) w_b in (query, head) order.  The other
+// workgroups merge the output rows, one per wave, alongside.
+template <int kRowPass>
+__global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a, int nsw) {
   __shared__ float wsh[kChunk * NH * kMassBlk];  // w_b of the group's blocks
   __shared__ float mi[kChunk * NH][2];           // m, 1/l per row
+  __shared__ __attribute__((aligned(16))) float pw[kMassWaves][kRowPass * kPwStride];
   const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
   const int npr = a.Sq * NH;
   if ((int)blockIdx.x >= nsw) {
-    const int pr = ((int)blockIdx.x - nsw) * 4 + wv;
+    const int pr = ((int)blockIdx.x - nsw) * kMassWaves + wv;
     if (pr < npr) h2o_out_row(a, pr, lane);
     return;
   }
@@ -319,10 +323,11 @@ __global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
   int g = blockIdx.x;
   int b0 = g * kMassBlk;
   // a group's loads that do not wait for the weights: the numerators of the
-  // first query, the slot's position and mass
-  float ev0[NH], acc = 0.0f;
+  // first query, the slot's position and mass (threads below 256)
+  float ev0[NH] = {}, acc = 0.0f;
   int sp = 0;
   auto fetch = [&](int gg) {
+    if (wv >= 4) return;
     const int t = gg * 256 + tid;
     const int tc = t < a.n_live ? t : 0;
 #pragma unroll
@@ -334,34 +339,52 @@ __global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
   // ---- m and 1/l of every row (lane = block); the first group's w_b
   if (a.nblk <= 64) {
     const bool in = lane < a.nblk;
-    for (int r0 = wv; r0 < npr; r0 += 4 * kRowPass) {
-      float mbv[kRowPass], prod[kRowPass], cb[kRowPass], l[kRowPass];
+    for (int r0 = wv; r0 < npr; r0 += kMassWaves * kRowPass) {
+      float mbv[kRowPass], lt[kRowPass], cb[kRowPass], m[kRowPass];
 #pragma unroll
       for (int k = 0; k < kRowPass; k++) {
-        const int r = r0 + 4 * k;
+        const int r = r0 + kMassWaves * k;
         const bool ok = in && r < npr;
         mbv[k] = ok ? a.part_ml[((size_t)r * a.nblk + lane) * 2] : kNegInf;
-        prod[k] = ok ? a.part_l[(size_t)r * a.nblk + lane] : 0.0f;
+        lt[k] = ok ? a.part_l[(size_t)r * a.nblk + lane] : 0.0f;
       }
-      float m[kRowPass];
+      float* pwr = pw[wv];
 #pragma unroll
       for (int k = 0; k < kRowPass; k++) {
         m[k] = wave_max_fast(mbv[k]);
         cb[k] = mbv[k] == kNegInf ? 0.0f : exp_det(mbv[k] - m[k]);
-        prod[k] = prod[k] * cb[k];
-        l[k] = 0.0f;
+        pwr[k * kPwStride + lane] = lt[k] * cb[k];
       }
-      // l in block order, the rows' chains side by side
-      for (int b = 0; b < a.nblk; b++) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // lane k: l of row r0 + 16k in block order, 32 blocks per read.
+      // Entries past nblk up to the next multiple of 4 are +0 (0 * 0),
+      // which leave a sum of non-negative terms unchanged.
+      float lk = 0.0f;
+      if (lane < kRowPass) {
+        const f32x4* row = (const f32x4*)(pwr + lane * kPwStride);
+        const int nc = (a.nblk + 3) >> 2;
+        for (int h = 0; h < nc; h += 8) {
+          f32x4 rv[8];
 #pragma unroll
-        for (int k = 0; k < kRowPass; k++)
-          l[k] = l[k] + __builtin_bit_cast(
-                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prod[k]), b));
+          for (int c = 0; c < 8; c++) rv[c] = row[h + c];
+#pragma unroll
+          for (int c = 0; c < 8; c++) {
+            if (h + c < nc) {
+              lk = lk + rv[c][0];
+              lk = lk + rv[c][1];
+              lk = lk + rv[c][2];
+              lk = lk + rv[c][3];
+            }
+          }
+        }
       }
+      const float invk = 1.0f / lk;
 #pragma unroll
       for (int k = 0; k < kRowPass; k++) {
-        const int r = r0 + 4 * k;
-        const float inv = 1.0f / l[k];
+        const int r = r0 + kMassWaves * k;
+        const float inv = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, invk), k));
         if (r < npr) {
           if (lane == 0) {
             mi[r][0] = m[k];
@@ -372,7 +395,7 @@ __global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
       }
     }
   } else {
-    for (int r = wv; r < npr; r += 4) {
+    for (int r = wv; r < npr; r += kMassWaves) {
       const size_t rb = (size_t)r * a.nblk;
       float m = kNegInf;
       for (int c0 = 0; c0 < a.nblk; c0 += 64)
@@ -405,7 +428,7 @@ __global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
   __syncthreads();
   for (;;) {
     const int t = g * 256 + tid;
-    if (t < a.n_live) {
+    if (tid < 256 && t < a.n_live) {
       const int bl = (t >> 6) - b0;
       const bool re = t == placed;
       const int spt = re ? a.posj : sp;
@@ -431,7 +454,7 @@ __global__ __launch_bounds__(256) void k_h2o_mass(H2oArgs a, int nsw) {
     b0 = g * kMassBlk;
     fetch(g);
     __syncthreads();  // the previous group's weights are read
-    for (int x = tid; x < npr * kMassBlk; x += 256) {
+    for (int x = tid; x < npr * kMassBlk; x += kMassWaves * 64) {
       const int r = x / kMassBlk, b = b0 + x % kMassBlk;
       const float mb = b < a.nblk ? a.part_ml[((size_t)r * a.nblk + b) * 2] : kNegInf;
       const float cb = mb == kNegInf ? 0.0f : exp_det(mb - mi[r][0]);
@@ -496,7 +519,8 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     int st = launch_status();
     if (st) return st;
     const int nsw = std::min((n_live + 255) / 256, kMassMaxWg);
-    hipLaunchKernelGGL(k_h2o_mass, dim3(nsw + (sq * NH + 3) / 4), dim3(256), 0, s, a, nsw);
+    hipLaunchKernelGGL(k_h2o_mass<8>, dim3(nsw + (sq * NH + kMassWaves - 1) / kMassWaves),
+                       dim3(kMassWaves * 64), 0, s, a, nsw);
     if ((st = launch_status())) return st;
   }
   return CIA_OK;
@@ -561,7 +585,8 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
     a.slotpos_w = slot_pos;
   }
   const int nsw = std::min((n1 + 255) / 256, kMassMaxWg);
-  hipLaunchKernelGGL(k_h2o_mass, dim3(nsw + NH / 4), dim3(256), 0, s, a, nsw);
+  hipLaunchKernelGGL(k_h2o_mass<2>, dim3(nsw + NH / kMassWaves), dim3(kMassWaves * 64), 0, s, a,
+                     nsw);
   if ((st = launch_status())) return st;
   *n_live = n1;
   return CIA_OK;
