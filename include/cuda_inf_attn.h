@@ -226,8 +226,10 @@ int cia_h2o_place(const uint16_t* k, const uint16_t* v, uint8_t* kf,
  * reference) gains the attention mass of every (query, head) with the
  * deterministic rule below, so that the eviction order is reproducible:
  *   s(t) = fma chain over d ascending of q[d]*k(t)[d] from 0, times scale;
- *   m = max s; e = expdet(s - m); l = 64-lane strided sums, then a
- *   butterfly; p = e * (1/l); attn_sum[t] += p in (query, head) order.
+ *   per 64-slot block b: m_b = max s, e = expdet(s - m_b), l_b = the
+ *   e's xor-butterfly total; m = max m_b, c_b = expdet(m_b - m),
+ *   l = sum of l_b * c_b in ascending b; p = e * (c_b * (1/l));
+ *   attn_sum[t] += p in (query, head) order.
  * ws: device scratch of ws_bytes >= cia_h2o_workspace_bytes(S, n_live)
  * bytes (16-byte aligned); queries are processed 16 at a time through it. */
 int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uint8_t* vf,
