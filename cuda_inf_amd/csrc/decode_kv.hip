@@ -61,8 +61,10 @@
 //   - a device-scope atomic round trip: about 0.25 us idle, 0.4-0.5 us under
 //     the stream; the acknowledgement of agent-coherent stores about 0.6 us.
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "attn_range.h"
 #include "qk_prep.h"
@@ -178,6 +180,9 @@ struct DecArgs {
   float* pl;             // [32][nsplit] sum of exp(s - m)
   float* po;             // [32][nsplit][64] sum of exp(s - m) v
   int nsplit, chunk, total;
+  int sub;               // workgroups per split (> 1: each takes a share of one
+                         // split and the last to arrive merges the shares,
+                         // through part and cnt[g * kCntStride + split])
 };
 
 // ---------------------------------------------------------------- kernel
@@ -189,9 +194,12 @@ struct DecArgs {
 // (r + 1) nsplit / R); its FP8 waves share a split's groups when it has at
 // most 8 splits, else take whole splits, and each finished split (or share)
 // is written as (m, l, o) -- straight to pm / pl / po when the workgroup has
-// 8 splits or more (one wave per split), else through LDS and its merge.  Keys outside a
-// segment's range are masked.  block = 512 (no tail waves: the tail keys are
-// added by k_split_tail).
+// 8 splits or more (one wave per split), else through LDS and its merge.
+// With sub > 1 workgroups per split (fewer splits than ranges), workgroup r
+// takes share r % sub of split r / sub; the shares meet in part and the last
+// workgroup to arrive writes the split.  Keys outside a segment's range are
+// masked.  The tail keys (fp16 rows) of the splits a workgroup writes are
+// taken by its tail waves and folded in by the split's writer.
 template <bool kPrep, bool kSplit>
 __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
@@ -215,13 +223,30 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // takes one group (an FP8 wave with a one-group buffer in the LDS the
   // others leave free).  The rest return.
   const bool xw = !kSplit && w == kFpWaves && r != 0 && r <= a.ne;
-  if (w >= kFpWaves && (kSplit || (r != 0 && !xw))) return;
+  if (!kSplit && w >= kFpWaves && r != 0 && !xw) return;
   const float qscale = a.scale * kLog2e;
   // split mode: this workgroup's splits [s0, s0 + ns)
-  int s0 = 0, ns = 0;
+  int s0 = 0, ns = 0, sj = 0;
   if constexpr (kSplit) {
-    s0 = (int)(((unsigned)r * (unsigned)a.nsplit) / (unsigned)a.R);
-    ns = (int)(((unsigned)(r + 1) * (unsigned)a.nsplit) / (unsigned)a.R) - s0;
+    if (a.sub > 1) {
+      s0 = r / a.sub;
+      sj = r - s0 * a.sub;
+      ns = 1;
+    } else {
+      s0 = (int)(((unsigned)r * (unsigned)a.nsplit) / (unsigned)a.R);
+      ns = (int)(((unsigned)(r + 1) * (unsigned)a.nsplit) / (unsigned)a.R) - s0;
+    }
+  }
+  // split mode: the splits [tlo, thi] with tail keys (committed..qpos) that
+  // this workgroup writes (at most two: splits have 128 keys or more, the
+  // tail at most 64); its tail waves take those keys
+  int tlo = 1, thi = 0;
+  if constexpr (kSplit) {
+    if (a.committed < a.total) {
+      tlo = max(a.committed / a.chunk, s0);
+      thi = min(min((a.total - 1) / a.chunk, s0 + ns - 1), tlo + 1);
+    }
+    if (w >= kFpWaves && (tlo > thi || w >= kFpWaves + kTailWaves)) return;
   }
 
   // ================================================================ FP8 waves
@@ -251,6 +276,10 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         sb = sa + 1;
         part_k = lw - fw;
         part_i = w - fw;
+        if (a.sub > 1) {  // share sj of the split's sub * 8 wave shares
+          part_k = kFpWaves * a.sub;
+          part_i = sj * kFpWaves + w;
+        }
       } else {
         sa = s0 + (w * ns) / kFpWaves;
         sb = s0 + ((w + 1) * ns) / kFpWaves;
@@ -647,6 +676,56 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
       if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
     }
+  } else if constexpr (kSplit) {
+    // ================================================ split mode: tail waves
+    // wave i = query head 4g + i takes the tail keys of each split in
+    // [tlo, thi]: an (m, l, o) partial in log2 units, as the FP8 waves', in
+    // the extra wave's LDS buffer (unused here) for the split's writer.
+    // Scores lane = tail key (fp32 fma chain from the fp16 rows), o lane = dim.
+    const int i = w - kFpWaves, h = g * GQA + i;
+    const int tt = a.total - a.committed;
+    float* sT = (float*)(lds + kLdsX);  // [2][4][kPartRow]
+    float vv[G];
+#pragma unroll
+    for (int k = 0; k < G; k++) vv[k] = k < tt ? h2f(a.vtail[((size_t)k * NKV + g) * D + l]) : 0.f;
+    __builtin_amdgcn_s_barrier();  // B1 (the FP8 waves'; nothing to wait for here)
+    float sc = -1e30f;
+    if (l < tt) {
+      const uint16_t* kp = a.ktail + ((size_t)l * NKV + g) * D;
+      const uint16_t* qp = a.q + (size_t)h * D;
+      float acc = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; d += 8) {
+        const u32x4 kk = *(const u32x4*)(kp + d), qq = *(const u32x4*)(qp + d);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          acc = __builtin_fmaf(h2f((uint16_t)qq[e]), h2f((uint16_t)kk[e]), acc);
+          acc = __builtin_fmaf(h2f((uint16_t)(qq[e] >> 16)), h2f((uint16_t)(kk[e] >> 16)), acc);
+        }
+      }
+      sc = acc * qscale;
+    }
+    for (int sp = tlo; sp <= thi; sp++) {
+      // the split's tail keys, as tail rows [k0, k1)
+      const int k0 = max(a.committed, sp * a.chunk) - a.committed;
+      const int k1 = min(a.total, (sp + 1) * a.chunk) - a.committed;
+      const bool in = l >= k0 && l < k1;
+      const float mt = wave_max_fast(in ? sc : -1e30f);
+      const float p = in ? __builtin_amdgcn_exp2f(sc - mt) : 0.f;
+      const float lt = wave_sum_fast(p);
+      float ot = 0.f;
+#pragma unroll
+      for (int k = 0; k < G; k++) {
+        const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
+        ot = __builtin_fmaf(pk, vv[k], ot);  // (p is 0 outside [k0, k1), vv 0 past the tail)
+      }
+      float* row = sT + ((sp - tlo) * GQA + i) * kPartRow;
+      row[4 + l] = ot;
+      if (l == 0) {
+        row[0] = mt;
+        row[1] = lt;
+      }
+    }
   } else if constexpr (!kSplit) {
     // ============================================================ tail waves
     const int i = w - kFpWaves;  // query head 4g + i
@@ -781,6 +860,38 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // ================================================================ merge
   if (w >= kFpWaves) return;  // (tail waves: their partial is in LDS)
   if constexpr (kSplit) {
+    // the tail waves' partial of split sp (head i, dim d) folded into a
+    // split's (M, L, O) in log2 units
+    auto fold_tail = [&](int sp, int i, int d, float& M, float& L, float& O) {
+      const float* row = (const float*)(lds + kLdsX) + ((sp - tlo) * GQA + i) * kPartRow;
+      const float mt = row[0], lt = row[1], ot = row[4 + d];
+      const float Mn = __builtin_fmaxf(M, mt);
+      const float w0 = L > 0.f ? __builtin_amdgcn_exp2f(M - Mn) : 0.f;
+      const float w1 = __builtin_amdgcn_exp2f(mt - Mn);
+      L = __builtin_fmaf(L, w0, lt * w1);
+      O = __builtin_fmaf(O, w0, ot * w1);
+      M = Mn;
+    };
+    if (ns >= kFpWaves) {
+      // the FP8 waves wrote their splits straight out (before B2): waves
+      // 0-3 (head i = w, lane = dim) fold the tail into the tail splits
+      if (tlo > thi || tid >= GQA * D) return;
+      const int i = tid >> 6, d = tid & 63, h = g * GQA + i;
+      for (int sp = tlo; sp <= thi; sp++) {
+        const size_t pi = (size_t)h * a.nsplit + sp;
+        const float m0 = __hip_atomic_load(a.pm + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float l0 = __hip_atomic_load(a.pl + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float o0 = __hip_atomic_load(a.po + pi * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float M = l0 > 0.f ? m0 * kLog2e : -1e30f, L = l0, O = o0;
+        fold_tail(sp, i, d, M, L, O);
+        a.po[pi * D + d] = O;
+        if (d == 0) {
+          a.pm[pi] = L > 0.f ? M * kLn2 : -1e30f;
+          a.pl[pi] = L;
+        }
+      }
+      return;
+    }
     // splits shared by several waves (at most 7 splits here): merge the
     // shares of each, head i = tid / 64, dim d
     if (ns < kFpWaves && tid < GQA * D) {
@@ -796,11 +907,70 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
           Oacc = __builtin_fmaf(sO[(p * GQA + i) * D + d], wt, Oacc);
         }
         const int sp = s0 + j;
+        if (a.sub <= 1 && sp >= tlo && sp <= thi) fold_tail(sp, i, d, M, L, Oacc);
+        if (a.sub > 1) {
+          // this workgroup's share of the split, for the last to arrive
+          float* row = a.part + ((size_t)(g * kMaxRanges + r) * GQA + i) * kPartRow;
+          __hip_atomic_store(row + 4 + d, Oacc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (d == 0) {
+            __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have reached the agent
+          continue;
+        }
         a.po[((size_t)h * a.nsplit + sp) * D + d] = Oacc;
         if (d == 0) {
           a.pm[h * a.nsplit + sp] = L > 0.f ? M * kLn2 : -1e30f;
           a.pl[h * a.nsplit + sp] = L;
         }
+      }
+    }
+    if (a.sub <= 1) return;
+    __builtin_amdgcn_s_barrier();  // the workgroup's share stored
+    uint32_t* ctr = a.cnt + g * kCntStride + s0;
+    uint32_t* sticket = (uint32_t*)(lds + kLdsTicket);
+    if (tid == 0) *sticket = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    if (*sticket != (uint32_t)(a.sub - 1)) return;
+    // ---- the last share of split s0 to arrive: every share stored.  The
+    // counter goes back to zero for the next call.
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < GQA * D) {
+      const int i = tid >> 6, d = tid & 63, h = g * GQA + i;
+      const __amdgpu_buffer_rsrc_t rs =
+          buf_rsrc(a.part + (size_t)(g * kMaxRanges + s0 * a.sub) * GQA * kPartRow);
+      // shares 8 at a time (the loads of a batch go out together)
+      float M = -1e30f, L = 0.f, O = 0.f;
+      for (int p0 = 0; p0 < a.sub; p0 += 8) {
+        float mp[8], lp[8], op[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const int o = ((p0 + k < a.sub ? p0 + k : p0) * GQA + i) * kPartRow;
+          mp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, o * 4, 0, kCoherent));
+          lp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + 1) * 4, 0, kCoherent));
+          op[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + 4 + d) * 4, 0, kCoherent));
+        }
+        float Mb = M;
+#pragma unroll
+        for (int k = 0; k < 8; k++) Mb = p0 + k < a.sub ? __builtin_fmaxf(Mb, mp[k]) : Mb;
+        const float c = __builtin_amdgcn_exp2f(M - Mb);
+        L *= c;
+        O *= c;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const float wt = p0 + k < a.sub ? __builtin_amdgcn_exp2f(mp[k] - Mb) : 0.f;
+          L = __builtin_fmaf(lp[k], wt, L);
+          O = __builtin_fmaf(op[k], wt, O);
+        }
+        M = Mb;
+      }
+      if (s0 >= tlo && s0 <= thi) fold_tail(s0, i, d, M, L, O);
+      a.po[((size_t)h * a.nsplit + s0) * D + d] = O;
+      if (d == 0) {
+        a.pm[h * a.nsplit + s0] = L > 0.f ? M * kLn2 : -1e30f;
+        a.pl[h * a.nsplit + s0] = L;
       }
     }
     return;
@@ -890,62 +1060,6 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     for (int p = 0; p < kMaxRanges; p++)
       O = __builtin_fmaf(ov[p], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), p)), O);
     a.out[(size_t)(g * GQA + i) * D + lane] = f2h(O * (1.0f / L));
-  }
-}
-
-// The fp16 tail keys (committed..qpos) of the splits they fall in, merged
-// into the partials k_decode<false, true> wrote for those splits (the
-// reference's split kernel reads them with the committed keys,
-// engine.cu:417-444).  grid = 8 kv heads, block = 256: wave i takes query head
-// 4g + i, lane = tail key for the scores (fp32 from the fp16 rows), lane =
-// dim for o.
-__global__ __launch_bounds__(256) void k_split_tail(const uint16_t* __restrict__ q,
-                                                    const uint16_t* __restrict__ ktail,
-                                                    const uint16_t* __restrict__ vtail,
-                                                    int committed, int total, float scale,
-                                                    float* __restrict__ pm, float* __restrict__ pl,
-                                                    float* __restrict__ po, int nsplit, int chunk) {
-  const int g = blockIdx.x, i = threadIdx.x >> 6, l = threadIdx.x & 63, h = g * GQA + i;
-  const int tt = total - committed;
-  float sc = -1e30f;
-  if (l < tt) {
-    const uint16_t* kp = ktail + ((size_t)l * NKV + g) * D;
-    const uint16_t* qp = q + (size_t)h * D;
-    float acc = 0.f;
-#pragma unroll
-    for (int d = 0; d < D; d += 8) {
-      const u32x4 kk = *(const u32x4*)(kp + d), qq = *(const u32x4*)(qp + d);
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        acc = __builtin_fmaf(h2f((uint16_t)qq[e]), h2f((uint16_t)kk[e]), acc);
-        acc = __builtin_fmaf(h2f((uint16_t)(qq[e] >> 16)), h2f((uint16_t)(kk[e] >> 16)), acc);
-      }
-    }
-    sc = acc * scale;
-  }
-  const int sfirst = committed / chunk, slast = (total - 1) / chunk;
-  for (int sp = sfirst; sp <= slast; sp++) {
-    // this split's tail keys, as tail rows [k0, k1)
-    const int k0 = max(committed, sp * chunk) - committed;
-    const int k1 = min(total, (sp + 1) * chunk) - committed;
-    const bool in = l >= k0 && l < k1;
-    const float mt = wave_max(in ? sc : -1e30f);
-    const float p = in ? fast_exp(sc - mt) : 0.f;
-    const float lt = wave_sum(p);
-    float ot = 0.f;
-    for (int k = k0; k < k1; k++) {
-      const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
-      ot = __builtin_fmaf(pk, h2f(vtail[((size_t)k * NKV + g) * D + l]), ot);
-    }
-    const size_t pi = (size_t)h * nsplit + sp;
-    const float m0 = pm[pi], l0 = pl[pi];
-    const float M = __builtin_fmaxf(m0, mt);
-    const float w0 = l0 > 0.f ? fast_exp(m0 - M) : 0.f, w1 = fast_exp(mt - M);
-    po[pi * D + l] = __builtin_fmaf(po[pi * D + l], w0, ot * w1);
-    if (l == 0) {
-      pm[pi] = M;
-      pl[pi] = __builtin_fmaf(l0, w0, lt * w1);
-    }
   }
 }
 
@@ -1066,6 +1180,43 @@ int scratch_for_device(void** out, hipStream_t s) {
   return CIA_OK;
 }
 
+// The split entry's share workspace (the layout of cia_attn_decode's), one
+// per (device, stream): allocated and its counters cleared on the first call
+// on a stream, kept until the process ends.  Calls on one stream run in
+// order, and calls on different streams use different workspaces.
+std::mutex g_split_mu;
+std::map<std::pair<int, hipStream_t>, void*> g_split_ws;
+
+int split_ws_for_stream(void** out, hipStream_t s) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_hip_error(e);
+    return CIA_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  const auto key = std::make_pair(dev, s);
+  auto it = g_split_ws.find(key);
+  if (it == g_split_ws.end()) {
+    void* p = nullptr;
+    e = hipMalloc(&p, kWsBytes);
+    if (e != hipSuccess) {
+      set_hip_error(e);
+      return CIA_ERR_HIP;
+    }
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, s,
+                       (uint32_t*)((char*)p + kPartBytes), NKV * kCntStride);
+    const int st = launch_status();
+    if (st) {
+      (void)hipFree(p);
+      return st;
+    }
+    it = g_split_ws.emplace(key, p).first;
+  }
+  *out = it->second;
+  return CIA_OK;
+}
+
 }  // namespace
 
 extern "C" int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
@@ -1089,18 +1240,28 @@ extern "C" int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, co
                          nullptr);
 }
 
-// The reference's split partials on the matrix cores (no workspace: every
-// split is finished inside one workgroup): k_decode<false, true> over the
-// committed keys, then k_split_tail for the tail keys.  Internal entry of
+// The reference's split partials on the matrix cores, one launch of
+// k_decode<false, true> (the tail keys folded in by the split's writer).
+// Fewer splits than ranges are each spread over several workgroups, which
+// meet in a workspace the library holds per stream.  Internal entry of
 // cia_attn_decode_split for nsplit <= kSplitMfmaMax (arguments checked there).
 extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed, int qpos,
     float scale, float* pm, float* pl, float* po, int nsplit, void* stream) {
   const int total = qpos + 1, chunk = (total + nsplit - 1) / nsplit;
-  int R = nsplit < kMaxRanges ? nsplit : kMaxRanges;
+  // workgroups per kv head: up to one per 8 CUs; fewer splits than that
+  // are each spread over sub workgroups
+  int cap = kMaxRanges;
   const int cus = device_cus();
-  if (cus > 0 && cus / NKV < R) R = cus / NKV > 0 ? cus / NKV : 1;
+  if (cus > 0 && cus / NKV < cap) cap = cus / NKV > 0 ? cus / NKV : 1;
+  const int sub = nsplit < cap ? cap / nsplit : 1;
+  const int R = nsplit < cap ? nsplit * sub : cap;
+  void* ws = nullptr;
+  if (sub > 1) {
+    const int st = split_ws_for_stream(&ws, (hipStream_t)stream);
+    if (st) return st;
+  }
   DecArgs da{};
   da.q = q;
   da.kc8 = (uint8_t*)kc8;
@@ -1120,11 +1281,10 @@ extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
   da.nsplit = nsplit;
   da.chunk = chunk;
   da.total = total;
+  da.sub = sub;
+  da.part = (float*)ws;
+  da.cnt = ws ? (uint32_t*)((char*)ws + kPartBytes) : nullptr;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((k_decode<false, true>), dim3(NKV * R), dim3(64 * kFpWaves), 0, s, da);
-  int st = launch_status();
-  if (st || committed >= total) return st;
-  hipLaunchKernelGGL(k_split_tail, dim3(NKV), dim3(256), 0, s, q, ktail, vtail, committed, total,
-                     scale, pm, pl, po, nsplit, chunk);
+  hipLaunchKernelGGL((k_decode<false, true>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
   return launch_status();
 }
