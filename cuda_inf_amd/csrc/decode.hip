@@ -43,51 +43,79 @@ __global__ __launch_bounds__(256) void k_decode_split(const uint16_t* __restrict
 // engine.cu:467-480 with runtime nsplit: the same merge (global max over the
 // splits' m, splits with l <= 0 skipped, exp weights), spread over 4 blocks
 // per query head (16 dims each) of 1024 threads: thread (group j, lane e)
-// sums splits j, j + 64, ... of dim 16 (blockIdx.y) + e, then the 64 sums
-// are added in LDS.  grid = (32 heads, 4).
+// takes splits j, j + 64, ... of dim 16 (blockIdx.y) + e, the first four
+// loaded before anything waits on them; the 4 groups of a wave are added
+// with permlane swaps, then the 16 waves' sums in LDS.  grid = (32 heads, 4).
 constexpr int kCombThreads = 1024;
 constexpr int kCombDims = 16;
 constexpr int kCombGroups = kCombThreads / kCombDims;
+constexpr int kCombPre = 4;  // splits per thread held in registers
 
 __global__ __launch_bounds__(kCombThreads) void k_decode_combine(const float* __restrict__ pm,
                                                                  const float* __restrict__ pl,
                                                                  const float* __restrict__ po,
                                                                  uint16_t* __restrict__ out,
                                                                  int nsplit) {
-  __shared__ float sacc[kCombGroups * kCombDims];
-  __shared__ float sred[kCombThreads / 64];
-  __shared__ float sl[kCombGroups];
-  const int h = blockIdx.x, tid = threadIdx.x;
+  constexpr int kWaves = kCombThreads / 64;
+  __shared__ float sred[kWaves];
+  __shared__ float sacc[kWaves][kCombDims];
+  __shared__ float sl[kWaves];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int e = tid % kCombDims, j = tid / kCombDims, d = blockIdx.y * kCombDims + e;
   const float* hm = pm + (size_t)h * nsplit;
   const float* hl = pl + (size_t)h * nsplit;
   const float* ho = po + (size_t)h * nsplit * D;
+  float mv[kCombPre], lv[kCombPre], ov[kCombPre];
+#pragma unroll
+  for (int k = 0; k < kCombPre; k++) {
+    const int s = j + kCombGroups * k;
+    const int sc = s < nsplit ? s : 0;
+    mv[k] = s < nsplit ? hm[sc] : -1e30f;
+    lv[k] = s < nsplit ? hl[sc] : 0.f;
+    ov[k] = s < nsplit ? ho[(size_t)sc * D + d] : 0.f;
+  }
   float gm = -1e30f;
-  for (int s = tid; s < nsplit; s += kCombThreads) gm = __builtin_fmaxf(gm, hm[s]);
-  gm = wave_max(gm);
-  if ((tid & 63) == 0) sred[tid >> 6] = gm;
+#pragma unroll
+  for (int k = 0; k < kCombPre; k++) gm = __builtin_fmaxf(gm, mv[k]);
+  for (int s = j + kCombGroups * kCombPre; s < nsplit; s += kCombGroups)
+    gm = __builtin_fmaxf(gm, hm[s]);
+  gm = wave_max_fast(gm);
+  if (lane == 0) sred[wv] = gm;
   __syncthreads();
   gm = sred[0];
 #pragma unroll
-  for (int k = 1; k < kCombThreads / 64; k++) gm = __builtin_fmaxf(gm, sred[k]);
+  for (int k = 1; k < kWaves; k++) gm = __builtin_fmaxf(gm, sred[k]);
   float l = 0.f, acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kCombPre; k++) {
+    if (lv[k] > 0.f) {
+      const float w = fast_exp(mv[k] - gm);
+      l = __builtin_fmaf(lv[k], w, l);
+      acc = __builtin_fmaf(ov[k], w, acc);
+    }
+  }
 #pragma unroll 4
-  for (int s = j; s < nsplit; s += kCombGroups) {
+  for (int s = j + kCombGroups * kCombPre; s < nsplit; s += kCombGroups) {
     const float ls = hl[s];
     if (ls <= 0.f) continue;
     const float w = fast_exp(hm[s] - gm);
     l = __builtin_fmaf(ls, w, l);
     acc = __builtin_fmaf(ho[(size_t)s * D + d], w, acc);
   }
-  sacc[j * kCombDims + e] = acc;
-  if (e == 0) sl[j] = l;
+  // lanes e, e + 16, e + 32, e + 48 of a wave hold its 4 groups of dim e
+  acc = col4_sum(acc);
+  l = col4_sum(l);
+  if (lane < kCombDims) {
+    sacc[wv][lane] = acc;
+    if (lane == 0) sl[wv] = l;
+  }
   __syncthreads();
   if (tid < kCombDims) {
     float L = 0.f, A = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < kCombGroups; k++) {
+#pragma unroll
+    for (int k = 0; k < kWaves; k++) {
       L += sl[k];
-      A += sacc[k * kCombDims + tid];
+      A += sacc[k][tid];
     }
     out[h * D + blockIdx.y * kCombDims + tid] = f2h(A / L);
   }
