@@ -132,7 +132,11 @@ int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
  * per query head.  Writes the partial softmax state (m, l, o) of every
  * (query head, split) to pm/pl/po at index h*nsplit + split.  An empty
  * split writes m = -1e30, l = 0.  nsplit in [1, CIA_NSPLIT_MAX]
- * (the reference fixes 16). */
+ * (the reference fixes 16).  With fewer splits than the launch has
+ * workgroups per kv head, each split is shared by several workgroups that
+ * meet in a device workspace the library allocates on the first call on a
+ * stream (per device and stream, about 280 KB, kept until the process
+ * ends): that first call is not capturable into a graph. */
 int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
                           const uint8_t* vc8, const uint16_t* ksc,
                           const uint16_t* vsc, const uint16_t* ktail,
