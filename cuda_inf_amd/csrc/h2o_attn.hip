@@ -101,12 +101,33 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2_t;
+
+// ds_read_b64_tr_b8: within each 16-lane block, lane i receives byte i mod 8
+// of the 8-byte rows addressed by lanes 2j + (i div 8), j = 0..7
+__device__ __forceinline__ u32x2 lds_read_tr8(const uint8_t* p) {
+  const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)p);
+  return u32x2{(uint32_t)v[0], (uint32_t)v[1]};
+}
+
+// 8 E4M3 bytes -> fp16, exactly (scale 1)
+__device__ __forceinline__ f16x8 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // grid = (nblk, 8, Sq), block = 256 (wave w: query head 4 kvh + w).  All
 // global loads are issued before the first use, so the kernel waits on
 // memory once.  kPlace (Sq = 1): the token is placed here (H2oPlace).
 template <bool kPlace>
 __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   __shared__ __attribute__((aligned(16))) uint8_t vl[64 * D];  // V rows of the block's slots, this kv head
+  __shared__ __attribute__((aligned(16))) _Float16 wl[GQA][64];  // each head's numerators (fp16)
+  __shared__ __attribute__((aligned(16))) _Float16 vsl[64];      // the slots' V scales
   __shared__ __attribute__((aligned(16))) uint8_t newkv[2][D];  // kPlace: the token's K / V bytes
   __shared__ uint16_t newsc[2];
   __shared__ uint64_t red[2][4];
@@ -240,18 +261,35 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   const float ed = ok ? exp_det(s - mb) : 0.0f;
   a.sc[((size_t)i * NH + h) * (a.nblk * 64) + t] = ed;
   const float lbd = wave_tree_sum(ed);  // the rule's butterfly total
-  // the block's partial softmax for the output
-  const float e = ok ? fast_exp(s - mb) : 0.0f;
-  const float lb = wave_sum_fast(e);
-  const float wgt = ok ? e * h2f(vs16) : 0.0f;
-  __syncthreads();  // V rows staged
-  float o = 0.0f;
-#pragma unroll 16
-  for (int j = 0; j < 64; j++) {
-    const float wj = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
-    o = __builtin_fmaf(wj, e4m3_to_f32<0>(vl[j * D + lane]), o);
+  // the block's partial softmax for the output: numerators e in fp16 (the
+  // sum taken over the same fp16 values), o = sum_t e(t) (V(t) * scale(t))
+  // on the matrix cores with each V row times its slot's scale in fp16
+  const _Float16 e16 = (_Float16)(ok ? fast_exp(s - mb) : 0.0f);
+  const float lb = wave_sum_fast((float)e16);
+  wl[wave_id()][lane] = e16;
+  if (wave_id() == 0) vsl[lane] = __builtin_bit_cast(_Float16, vs16);
+  __syncthreads();  // V rows, numerators and scales in LDS
+  // O (16 rows, all the same) = W (64 numerators in every row) x V' (64
+  // slots x 64 dims): A lane (r, kg) holds slots 32 s + 8 kg .. +7, B lane
+  // (n, kg) the same slots of dim 16 dt + n (a transposing read), so lane l
+  // ends with dim l in element 0 of product dt = l / 16
+  const int kg = lane >> 4, ln = lane & 15;
+  f32x4 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    const int sl0 = 32 * ks + 8 * kg;
+    const f16x8 wa = *(const f16x8*)&wl[wave_id()][sl0];
+    const f16x8 sc8 = *(const f16x8*)&vsl[sl0];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      const u32x2 raw = lds_read_tr8(vl + (sl0 + (ln >> 1)) * D + 16 * dt + 8 * (ln & 1));
+      const f16x8 vb = e4m3x8_to_f16(raw[0], raw[1]) * sc8;
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, vb, acc[dt], 0, 0, 0);
+    }
   }
+  const float o = kg == 0 ? acc[0][0] : (kg == 1 ? acc[1][0] : (kg == 2 ? acc[2][0] : acc[3][0]));
   const size_t pi = ((size_t)i * NH + h) * a.nblk + blk;
   a.part_o[pi * D + lane] = o;
   if (lane == 0) {
