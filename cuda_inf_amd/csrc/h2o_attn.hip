@@ -70,6 +70,11 @@ struct H2oArgs {
   const int32_t* placed;
   int32_t* slotpos_w;
   int posj;
+  // single-token step: the placement keys of the next step, per slot-owning
+  // wave (min (mass, slot) key among its slots with position <= klim, and
+  // among all), for a next step at posj + 1 (klim = posj + 1 - W); null: none
+  uint64_t* keys;
+  int klim;
 };
 
 // Placement of a single fresh token inside the scores launch (the
@@ -95,6 +100,10 @@ struct H2oPlace {
   int32_t* slotpos;
   int32_t* dst;  // dst[0] = the slot, -1 when none can be taken
   int n0, C, W, posj;
+  // the previous step's mass launch's keys of this step's buffer (nkw
+  // pairs), or null: then every workgroup reads all masses and positions
+  const uint64_t* keys;
+  int nkw;
 };
 
 __device__ __forceinline__ int wave_id() {
@@ -144,7 +153,12 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   if constexpr (kPlace) {
     tk = h2f(pl.k[kvh * D + lane]);
     tv = h2f(pl.v[kvh * D + lane]);
-    if (pl.n0 >= pl.C) {
+    if (pl.n0 >= pl.C && pl.keys) {
+      for (int x = tid; x < pl.nkw; x += 256) {
+        kwin = min_u64(kwin, pl.keys[2 * x]);
+        kall = min_u64(kall, pl.keys[2 * x + 1]);
+      }
+    } else if (pl.n0 >= pl.C) {
       const int lim = pl.posj - pl.W;
       for (int u0 = tid; u0 < pl.C; u0 += 256 * 8) {
         float m[8];
@@ -464,6 +478,7 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a, int nsw) {
     }
   }
   __syncthreads();
+  uint64_t kwin = ~0ull, kall = ~0ull;  // the next step's placement keys (a.keys)
   for (;;) {
     const int t = g * 256 + tid;
     if (tid < 256 && t < a.n_live) {
@@ -485,6 +500,11 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a, int nsw) {
       }
       a.attn_sum[t] = x;
       if (re) a.slotpos_w[t] = a.posj;
+      if (a.keys && x < kPicked) {
+        const uint64_t key = place_key(x, t);
+        kall = min_u64(kall, key);
+        if (spt <= a.klim) kwin = min_u64(kwin, key);
+      }
     }
     g += nsw;
     if (g >= ng) break;
@@ -500,11 +520,25 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a, int nsw) {
     }
     __syncthreads();
   }
+  if (a.keys && wv < 4) {
+    // each slot-owning wave's minimum keys
+    kwin = wave_min_u64(kwin);
+    kall = wave_min_u64(kall);
+    if (lane == 0) {
+      a.keys[2 * (blockIdx.x * 4 + wv)] = kwin;
+      a.keys[2 * (blockIdx.x * 4 + wv) + 1] = kall;
+    }
+  }
+}
+
+// the placement keys' region after the partials (16-byte aligned)
+int64_t h2o_keys_offset(int S, int C) {
+  const int64_t sq = std::min(S, kChunk), nblk = (C + 63) / 64;
+  return (sq * NH * (2 * nblk * 64 + 3 * nblk) * (int64_t)sizeof(float) + 15) / 16 * 16;
 }
 
 int64_t h2o_ws_bytes(int S, int C) {
-  const int64_t sq = std::min(S, kChunk), nblk = (C + 63) / 64;
-  return sq * NH * (2 * nblk * 64 + 3 * nblk) * (int64_t)sizeof(float);
+  return h2o_keys_offset(S, C) + (int64_t)kMassMaxWg * 4 * 2 * sizeof(uint64_t);
 }
 
 }  // namespace cia
@@ -553,7 +587,11 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     a.placed = nullptr;
     a.slotpos_w = nullptr;
     a.posj = 0;
-    hipLaunchKernelGGL(k_h2o_scores<false>, dim3(nblk, NKV, sq), dim3(256), 0, s, a, H2oPlace{});
+    a.keys = nullptr;
+    a.klim = 0;
+    hipLaunchKernelGGL(k_h2o_scores<false>, dim3(nblk, NKV, sq), dim3(256), 0, s, a,
+                       H2oPlace{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                nullptr, nullptr, 0, 0, 0, 0, nullptr, 0});
     int st = launch_status();
     if (st) return st;
     const int nsw = std::min((n_live + 255) / 256, kMassMaxWg);
@@ -568,12 +606,17 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
 // quantised inside the scores launch (H2oPlace), then the mass launch.  The
 // same slots, positions, bytes and masses as cia_h2o_place followed by
 // cia_attention_h2o for S = 1.  mid_event (may be NULL) is recorded after
-// the scores launch.
+// the scores launch.  When the buffer is full after the step, the mass
+// launch also leaves in ws the placement keys of a next step at past + 1
+// with the same window; keys_valid says that the previous call on this
+// layer was such a step at past - 1 (and nothing else has touched the
+// buffer since), so the scores launch reads those keys instead of every
+// slot's mass and position.
 extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
     uint16_t* ks, uint16_t* vs, float* attn_sum, int32_t* slot_pos, int32_t* dst_slots,
     int* n_live, int C, int W, int past, uint16_t* out, float scale, void* ws, int64_t ws_bytes,
-    void* stream, void* mid_event) {
+    void* stream, void* mid_event, int keys_valid) {
   CIA_REQUIRE(n_live, CIA_ERR_NULL);
   CIA_REQUIRE(past >= 0 && C >= 1 && W >= 0 && *n_live >= 0 && *n_live <= C, CIA_ERR_ARG);
   CIA_REQUIRE(q && k && v && kf && vf && ks && vs && attn_sum && slot_pos && dst_slots && out && ws,
@@ -607,7 +650,13 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
   a.placed = nullptr;
   a.slotpos_w = nullptr;
   a.posj = past;
-  const H2oPlace pl{k, v, kf, vf, ks, vs, attn_sum, slot_pos, dst_slots, n0, C, W, past};
+  uint64_t* keys = (uint64_t*)((char*)ws + h2o_keys_offset(1, n1));
+  a.keys = n1 >= C ? keys : nullptr;
+  a.klim = past + 1 - W;
+  const H2oPlace pl{k,  v,  kf, vf, ks,   vs,
+                    attn_sum, slot_pos, dst_slots, n0, C, W, past,
+                    keys_valid && n0 >= C ? keys : nullptr,
+                    4 * std::min((n0 + 255) / 256, kMassMaxWg)};
   hipLaunchKernelGGL(k_h2o_scores<true>, dim3(nblk, NKV, 1), dim3(256), 0, s, a, pl);
   int st = launch_status();
   if (st) return st;

@@ -25,7 +25,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, uint8_t* kf, uint8_t* vf,
     uint16_t* ks, uint16_t* vs, float* attn_sum, int32_t* slot_pos, int32_t* dst_slots,
     int* n_live, int C, int W, int past, uint16_t* out, float scale, void* ws, int64_t ws_bytes,
-    void* stream, void* mid_event);
+    void* stream, void* mid_event, int keys_valid);
 
 extern "C" __attribute__((visibility("hidden"))) int cia_qk_prep_into(
     const uint16_t* q, const uint16_t* k, const uint16_t* qw, const uint16_t* kw, uint16_t* oq,
@@ -183,9 +183,12 @@ const void* layer_prep(const cia_layer* L) {
 
 // engine.cu:803-828 with the slot choice on the device: place + quantise,
 // then attention with the mass update; no host round trip
+// keys_valid: the previous call on L was a single-token step at past - 1
+// (within one cia_decode_loop call), whose mass launch left this step's
+// placement keys in L->ws_mass
 int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                 uint16_t* out, int S, int past, float scale, int* evicted, void* stream,
-                void* mid_event = nullptr) {
+                void* mid_event = nullptr, bool keys_valid = false) {
   const int C = L->budget;
   if (!L->kf || !L->vf || !L->ks || !L->vs || !L->hattn || !L->d_slotpos || !L->d_dst ||
       !L->ws_mass)
@@ -197,7 +200,7 @@ int h2o_forward(cia_layer* L, const uint16_t* q, const uint16_t* k, const uint16
     // one token: placed and quantised inside the attention's first launch
     st = cia_h2o_decode_step(q, k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos,
                              L->d_dst, &L->n_live, C, L->window, past, out, scale, L->ws_mass,
-                             cia_h2o_workspace_bytes(1, C), stream, mid_event);
+                             cia_h2o_workspace_bytes(1, C), stream, mid_event, keys_valid);
     if (st) return st;
   } else {
     st = cia_h2o_place(k, v, L->kf, L->vf, L->ks, L->vs, L->hattn, L->d_slotpos, L->d_dst,
@@ -330,7 +333,7 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
       if (L->budget > 0) {
         if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r], s)))) return st;
         st = h2o_forward(L, q + r * qrow, k + r * krow, v + r * krow, out + r * qrow, 1, pos,
-                         scale, nullptr, stream, events ? events[3 * r + 1] : nullptr);
+                         scale, nullptr, stream, events ? events[3 * r + 1] : nullptr, i > 0);
         if (st) return st;
         if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
         continue;

@@ -90,6 +90,37 @@ def test_h2o_eviction_golden(cia, dev):
     assert np.array_equal(L.d_slotpos.cpu().numpy(), g["slotpos"])
 
 
+def test_h2o_eviction_golden_decode_loop(cia, dev):
+    """The same 4000 steps through the C decode loop in two calls (2500 +
+    1500): from each call's second step on, a step's slot choice reads the
+    placement keys the previous step's mass launch left (8 slot workgroups
+    at 2048 slots), the first step of each call scans every slot.  Final
+    masses and positions bit-identical to the committed oracle run (a single
+    different eviction would change both)."""
+    import ctypes
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd._lib import call
+    g = np.load(GOLDEN, allow_pickle=False)
+    steps, C, W, P = int(g["steps"]), int(g["C"]), int(g["W"]), int(g["prompt"])
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "make_h2o_golden", os.path.join(os.path.dirname(GOLDEN), "make_h2o_golden.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    q, k, v = mk.inputs(steps)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    L = AttnLayer(P + steps + 4, budget=C, window=W, prompt_len=P, max_batch=P, device=dev)
+    L.forward(qd[:P], kd[:P], vd[:P], 0)
+    out = torch.zeros((P + steps, 32, 64), dtype=torch.float16, device=dev)
+    s = torch.cuda.current_stream()
+    for s0, n in ((P, 2500), (P + 2500, steps - 2500)):
+        call("cia_decode_loop", ctypes.byref(L._s), 1, qd[s0].data_ptr(), kd[s0].data_ptr(),
+             vd[s0].data_ptr(), out[s0].data_ptr(), s0, n, 0.125, None, s.cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(L.hattn.cpu().numpy().view(np.uint32), g["attn_sum"].view(np.uint32))
+    assert np.array_equal(L.d_slotpos.cpu().numpy(), g["slotpos"])
+
+
 # (C, W, n_live, S, past, attn kind): fill only, fill then evict, the window
 # empty (fallback scan), more than one slot per thread, signed zeros and NaN
 # masses, an unfused batch of evictions
