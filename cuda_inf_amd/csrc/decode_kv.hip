@@ -685,10 +685,15 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     const int i = w - kFpWaves, h = g * GQA + i;
     const int tt = a.total - a.committed;
     float* sT = (float*)(lds + kLdsX);  // [2][4][kPartRow]
-    float vv[G];
-#pragma unroll
-    for (int k = 0; k < G; k++) vv[k] = k < tt ? h2f(a.vtail[((size_t)k * NKV + g) * D + l]) : 0.f;
+    // B1 first: the FP8 waves' streams wait on it, and nothing here is needed there
     __builtin_amdgcn_s_barrier();  // B1 (the FP8 waves'; nothing to wait for here)
+    // V rows of the tail (lane = dim): every load out before any is used, so
+    // they take one round trip.  All 64 rows of the tail buffer are read (one
+    // base, constant row offsets); rows past the tail are dropped below.
+    uint16_t vr[G];
+    const uint16_t* vt = a.vtail + (size_t)g * D + l;
+#pragma unroll
+    for (int k = 0; k < G; k++) vr[k] = vt[(size_t)k * NKV * D];
     float sc = -1e30f;
     if (l < tt) {
       const uint16_t* kp = a.ktail + ((size_t)l * NKV + g) * D;
@@ -705,6 +710,9 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
       sc = acc * qscale;
     }
+    float vv[G];
+#pragma unroll
+    for (int k = 0; k < G; k++) vv[k] = k < tt ? h2f(vr[k]) : 0.f;
     for (int sp = tlo; sp <= thi; sp++) {
       // the split's tail keys, as tail rows [k0, k1)
       const int k0 = max(a.committed, sp * a.chunk) - a.committed;

@@ -224,6 +224,36 @@ def test_split_combine_131k(orc, cia, dev, cache131k, nsplit):
     _check_partials(pm, pl, po, rpm, rpl, rpo)
 
 
+def test_split_combine_131k_tail(orc, cia, dev, cache131k):
+    """The long-context shape of the split leg: 131072 committed keys and a
+    9-key tail, 16 splits of 8193 keys (splits 0-14 each touch 129 groups,
+    the last split holds the tail keys).  Appends to the shared cache, so it
+    runs after the other 131k tests."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.workload import qkv
+    L, ref = cache131k
+    n = 131072
+    if not getattr(ref, "tail9", False):
+        _, k, v = qkv(9, seed=4242, device="cpu", past=n, outliers=True)
+        _append(L, k, v, n, dev)
+        ref.append(_u16(k), _u16(v), n)
+        ref.tail9 = True
+    assert L.committed == ref.committed == n
+    qpos, nsplit = n + 8, 16
+    q, _, _ = qkv(1, seed=991, device="cpu", past=qpos)
+    pm = torch.full((32 * nsplit,), 7.0, device=dev)
+    pl = torch.full((32 * nsplit,), 7.0, device=dev)
+    po = torch.full((32 * nsplit * 64,), 7.0, device=dev)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    K.attn_decode_split(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed,
+                        qpos, 0.125, pm, pl, po, nsplit)
+    K.attn_decode_combine(pm, pl, po, out, nsplit)
+    torch.cuda.synchronize()
+    _, r32, (rpm, rpl, rpo) = orc.attn_decode(_u16(q), ref, qpos, nsplit=nsplit, nthreads=8)
+    assert_close_f16(_u16(out), r32)
+    _check_partials(pm, pl, po, rpm, rpl, rpo)
+
+
 def test_append_4096_bit_exact(orc, cia, dev):
     from cuda_inf_amd.layer import AttnLayer
     from cuda_inf_amd.workload import qkv
@@ -244,12 +274,15 @@ def test_append_4096_bit_exact(orc, cia, dev):
 
 @pytest.mark.parametrize("ntok,nsplit", [(10109, 76), (25700, 200), (70000, 300), (2032, 7),
                                          (5000, 3), (4300, 33), (200, 1), (3000, 1), (4096, 16),
-                                         (2032, 40), (777, 512), (64, 16), (131, 300), (1, 1)])
+                                         (2032, 40), (777, 512), (64, 16), (131, 300), (1, 1),
+                                         (33000, 16), (70001, 7)])
 def test_split_partials_geometry(orc, cia, dev, ntok, nsplit):
     """Split geometries.  Matrix-core path (splits of 128 keys or more): the
     tail straddling two splits (10109 / 76, 25700 / 200, and 70000 / 300 with
     more than 8 splits per workgroup), odd workgroups per kv head (7, 3, 33),
-    one workgroup per kv head (nsplit 1), no tail (4096).  Splits of fewer
+    one workgroup per kv head (nsplit 1), no tail (4096); splits that start
+    inside a group and are shared by several workgroups (33000 / 16: 33 or 34
+    groups over 2 workgroups per split; 70001 / 7: 157 or 158 over 4).  Splits of fewer
     keys take the fp32 kernel: 2032 / 40, 777 / 512 and 131 / 300 (few keys,
     empty splits), 64 / 16, and no committed group (1).  Every partial against
     the oracle's, empty splits exactly (-1e30, 0, 0)."""
