@@ -6,12 +6,15 @@
 // ride along).
 //
 // Work split.  Workgroup = (kv head g, key range r); 8R workgroups, R ranges
-// per kv head (R = 1, or even and at most 32).  Workgroups go to the 8 XCDs
-// round-robin (XCD = blockIdx mod 8), and the numbering puts kv heads 2j and
-// 2j + 1 of the same range on one XCD: a kv head's 64 bytes are half of a
-// 128-byte line, and when the two halves are fetched by different XCDs
-// every line crosses the fabric twice (measured: a plain read of the same
-// bytes at half the rate).
+// per kv head on average (R = 1, or even and at most 32).  Workgroups go to
+// the 8 XCDs round-robin (XCD = blockIdx mod 8), and the numbering puts kv
+// heads 2j and 2j + 1 of the same range on one XCD: a kv head's 64 bytes are
+// half of a 128-byte line, and when the two halves are fetched by different
+// XCDs every line crosses the fabric twice (measured: a plain read of the
+// same bytes at half the rate).  On long streams the head pair whose bytes
+// sit at 384..511 of each 512-byte block (a quarter of the cache that
+// streams about a third slower) gets more ranges than the other three pairs
+// (41 against 29 at R = 32), so that its workgroups end with the others'.
 //
 // FP8 waves (8 per workgroup).  The committed groups of kv head g are
 // spread evenly over the 8R waves of the kv head (whole 64-key groups), and
@@ -74,7 +77,7 @@ namespace cia {
 constexpr int kFpWaves = 8;                // FP8 waves per workgroup
 constexpr int kTailWaves = GQA;            // tail waves (workgroup of range 0)
 constexpr int kDecThreads = 64 * (kFpWaves + kTailWaves);
-constexpr int kMaxRanges = 32;             // workgroups per kv head
+constexpr int kMaxRanges = 44;             // workgroups per kv head (32 on average)
 constexpr int kBlkB = 16 * 64 + 16;        // 16 keys x 64 B + 16 B pad
 constexpr int kTileB = 4 * kBlkB;          // one 64-key group of one kv head
 constexpr int kHalfB = 2 * kTileB;         // K (or V) of a unit
@@ -174,6 +177,10 @@ struct DecArgs {
   int R;                 // workgroups per kv head
   int ne;                // extra groups: the last ne groups, one each to wave 8
                          // of workgroups 1..ne
+  // decode mode, unequal ranges: kv heads 2p and 2p + 1 have rp[p]
+  // workgroups each (extra groups nep[p]); up = prefix sums of rp.  rp[0] = 0:
+  // R and ne for every head.
+  int rp[4], up[5], nep[4];
   QkPrep prep;
   // split mode (the reference's attn_decode_split partials, committed keys only)
   float* pm;             // [32][nsplit] max score (natural units), -1e30 when empty
@@ -209,10 +216,20 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   f32x2* sml = (f32x2*)(lds + kLdsML);  // [p][i] at p * 4 + i
 
   const int bx = blockIdx.x, xcd = bx & 7, yy = bx >> 3;
-  int g, r;
+  int g, r, R = a.R, ne = a.ne;
   if (a.R == 1 || (kSplit && (a.R & 1))) {
     g = xcd;
     r = yy;
+  } else if (!kSplit && a.rp[0] > 0) {
+    // pair units: workgroups 16j + x and 16j + 8 + x (one XCD) take kv heads
+    // 2p and 2p + 1 over the same range; XCD x holds units R/2 x .. R/2 x +
+    // R/2 - 1 of the 4R, which go to the pairs in order, rp[p] each
+    const int U = xcd * (a.R >> 1) + (yy >> 1);
+    const int p = U >= a.up[2] ? (U >= a.up[3] ? 3 : 2) : (U >= a.up[1] ? 1 : 0);
+    g = 2 * p + (yy & 1);
+    r = U - a.up[p];
+    R = a.rp[p];
+    ne = a.nep[p];
   } else {
     g = 2 * (xcd & 3) + (yy & 1);
     r = (xcd >> 2) * (a.R >> 1) + (yy >> 1);
@@ -222,7 +239,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // Wave 8: a tail wave in range 0; in ranges 1..ne the extra wave, which
   // takes one group (an FP8 wave with a one-group buffer in the LDS the
   // others leave free).  The rest return.
-  const bool xw = !kSplit && w == kFpWaves && r != 0 && r <= a.ne;
+  const bool xw = !kSplit && w == kFpWaves && r != 0 && r <= ne;
   if (!kSplit && w >= kFpWaves && r != 0 && !xw) return;
   const float qscale = a.scale * kLog2e;
   // split mode: this workgroup's splits [s0, s0 + ns)
@@ -252,7 +269,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // ================================================================ FP8 waves
   if (w < kFpWaves || xw) {
     const int n = l & 15, c = l >> 4;  // MFMA column / k-group of this lane
-    const int om = r * kFpWaves + w, nwv = a.R * kFpWaves, ngm = a.ng - a.ne;
+    const int om = r * kFpWaves + w, nwv = R * kFpWaves, ngm = a.ng - ne;
     // this wave's committed groups [g0, g1), taken two at a time from g0 (a
     // unit: groups s and s + 1; the second masked when s + 1 == g1); the
     // extra wave's: group ngm + r - 1
@@ -983,12 +1000,11 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     }
     return;
   }
-  const int R = a.R;
   float* pg = a.part + (size_t)g * kMaxRanges * kPartF;  // kv head g's partials
   if (tid < GQA * D) {
     // the workgroup's partial of (head 4g + i, dim d)
     const int i = tid >> 6, d = tid & 63;
-    const int np = r == 0 || r <= a.ne ? kFpWaves + 1 : kFpWaves;
+    const int np = r == 0 || r <= ne ? kFpWaves + 1 : kFpWaves;
     // (every read first, then the arithmetic: the reads go out together)
     f32x2 ml[kFpWaves + 1];
     float ov[kFpWaves + 1];
@@ -1054,20 +1070,29 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   if (tid < GQA * D) {
     // wave i = query head 4g + i: lane p weighs partial p, then lane d sums
     // dim d (the row reads go out together; the weights come from lane p)
+    // (NP: 32 partials, or kMaxRanges for the unequal ranges; the terms past
+    // R weigh 0 and leave the sum's bits as they are)
     const int i = w, lane = l;
-    const f32x2 mlp = *(const f32x2*)(sp + (size_t)((lane < R ? lane : 0) * GQA + i) * kPartRow);
-    float ov[kMaxRanges];
+    auto finish = [&](auto np_tag) {
+      constexpr int NP = decltype(np_tag)::value;
+      const f32x2 mlp = *(const f32x2*)(sp + (size_t)((lane < R ? lane : 0) * GQA + i) * kPartRow);
+      float ov[NP];
 #pragma unroll
-    for (int p = 0; p < kMaxRanges; p++) ov[p] = sp[((p < R ? p : 0) * GQA + i) * kPartRow + 4 + lane];
-    const bool ok = lane < R && mlp[1] > 0.f;
-    const float M = wave_max_fast(ok ? mlp[0] : -1e30f);
-    const float wt = ok ? __builtin_amdgcn_exp2f(mlp[0] - M) : 0.f;
-    const float L = wave_sum_fast(ok ? mlp[1] * wt : 0.f);
-    float O = 0.f;
+      for (int p = 0; p < NP; p++) ov[p] = sp[((p < R ? p : 0) * GQA + i) * kPartRow + 4 + lane];
+      const bool ok = lane < R && mlp[1] > 0.f;
+      const float M = wave_max_fast(ok ? mlp[0] : -1e30f);
+      const float wt = ok ? __builtin_amdgcn_exp2f(mlp[0] - M) : 0.f;
+      const float L = wave_sum_fast(ok ? mlp[1] * wt : 0.f);
+      float O = 0.f;
 #pragma unroll
-    for (int p = 0; p < kMaxRanges; p++)
-      O = __builtin_fmaf(ov[p], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), p)), O);
-    a.out[(size_t)(g * GQA + i) * D + lane] = f2h(O * (1.0f / L));
+      for (int p = 0; p < NP; p++)
+        O = __builtin_fmaf(ov[p], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), p)), O);
+      a.out[(size_t)(g * GQA + i) * D + lane] = f2h(O * (1.0f / L));
+    };
+    if (R <= 32)
+      finish(std::integral_constant<int, 32>{});
+    else
+      finish(std::integral_constant<int, kMaxRanges>{});
   }
 }
 
@@ -1102,6 +1127,53 @@ static int dec_ranges(int ng) {
   return R > cap ? cap : R;
 }
 
+// The head pair whose bytes sit at 384..511 of each 512-byte block of the
+// cache (kv heads 2p and 2p + 1 own bytes 128p .. 128p + 127 of a key's
+// 512-byte row).  Measured on MI355X with per-wave timestamps: the
+// workgroups reading that quarter get their first data 1-1.5 us later and
+// take about a third longer over the same bytes (stream ends 24.5 against
+// 18.5 us at 131072 keys), from HBM and from the Infinity Cache alike; the
+// slow heads move with the buffers' base address (bases 128 or 256 bytes
+// further on make heads 4-5 or 2-3 the slow pair instead of 6-7).  -1 when K and V disagree or a base
+// is not 128-byte aligned.
+static int slow_pair(const void* kc8, const void* vc8) {
+  const uintptr_t k = (uintptr_t)kc8 & 511, v = (uintptr_t)vc8 & 511;
+  if (k != v || (k & 127)) return -1;
+  return (int)(((384 - k) & 511) >> 7);
+}
+
+// Workgroups per head pair for R per kv head on average (4R units of two
+// workgroups), once the stream is long (2 or more two-group units per FP8
+// wave on average: a workgroup's time then follows its bytes, its waves
+// sharing the CU's bandwidth): the slow pair gets rs, the others
+// (4R - rs) / 3, with rs the feasible count that minimises the costliest
+// workgroup's groups weighed 7/5 for the slow pair.  Shorter streams, or no
+// slow pair: equal ranges (rp[0] = 0).
+static void pair_ranges(int ng, int R, int slow, DecArgs& da) {
+  da.rp[0] = 0;
+  if (slow < 0 || R < 8 || ng < 4 * kFpWaves * R) return;
+  int best_rs = R;
+  double best = 7.0 / R;
+  for (int rs = R + 3; rs <= kMaxRanges && 4 * R - rs >= 3; rs += 3) {
+    const int rf = (4 * R - rs) / 3;
+    const double c = std::max(5.0 / rf, 7.0 / rs);
+    if (c < best) {
+      best = c;
+      best_rs = rs;
+    }
+  }
+  if (best_rs == R) return;
+  const int rf = (4 * R - best_rs) / 3;
+  int acc = 0;
+  for (int p = 0; p < 4; p++) {
+    da.rp[p] = p == slow ? best_rs : rf;
+    da.nep[p] = std::min(std::max(ng - 16 * da.rp[p], 0), da.rp[p] - 1);
+    da.up[p] = acc;
+    acc += da.rp[p];
+  }
+  da.up[4] = acc;
+}
+
 extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
   return max_tokens < 0 ? 0 : kWsBytes;
 }
@@ -1124,7 +1196,8 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   const int ne = R > 1 ? std::min(std::max(ng - 16 * R, 0), R - 1) : 0;
   DecArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail,
              knew, vnew, committed, qpos, scale, (float*)ws,
-             (uint32_t*)((char*)ws + kPartBytes), out, ng, R, ne, QkPrep{}};
+             (uint32_t*)((char*)ws + kPartBytes), out, ng, R, ne, {}, {}, {}, QkPrep{}};
+  pair_ranges(ng, R, slow_pair(kc8, vc8), da);
   if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
   if (da.prep.qw)

@@ -135,7 +135,7 @@ int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
  * (the reference fixes 16).  With fewer splits than the launch has
  * workgroups per kv head, each split is shared by several workgroups that
  * meet in a device workspace the library allocates on the first call on a
- * stream (per device and stream, about 280 KB, kept until the process
+ * stream (per device and stream, about 380 KB, kept until the process
  * ends): that first call is not capturable into a graph. */
 int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
                           const uint8_t* vc8, const uint16_t* ksc,
@@ -172,7 +172,7 @@ int64_t cia_decode_workspace_bytes(int max_tokens);
 /* cia_attn_decode without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * workspace is a fixed device array inside the library (274 KiB per GPU,
+ * workspace is a fixed device array inside the library (376 KiB per GPU,
  * held until the process ends; it covers every context); the call allocates
  * nothing.  Calls on one GPU share it: calls that overlap on one GPU
  * (several streams or host threads) race.  Same arguments, results and

@@ -224,6 +224,61 @@ def test_split_combine_131k(orc, cia, dev, cache131k, nsplit):
     _check_partials(pm, pl, po, rpm, rpl, rpo)
 
 
+def test_decode_131k(orc, cia, dev, cache131k):
+    """cia_attn_decode over the 131072-key cache (the long-context shape of the
+    matrix-core leg: unequal ranges per head pair, 38 workgroups for the pair
+    that owns the cache's slow 128-byte quarter, 30 for the others)."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.workload import qkv
+    L, ref = cache131k
+    qpos = L.committed - 1 + (9 if getattr(ref, "tail9", False) else 0)
+    q, _, _ = qkv(1, seed=515, device="cpu", past=qpos)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    ws = torch.zeros(K.decode_workspace_bytes(qpos + 1), dtype=torch.uint8, device=dev)
+    K.attn_decode(q.to(dev), L.kc8, L.vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed, qpos,
+                  0.125, out, ws)
+    torch.cuda.synchronize()
+    _, r32, _ = orc.attn_decode(_u16(q), ref, qpos, nsplit=16, nthreads=8)
+    assert_close_f16(_u16(out), r32)
+
+
+@pytest.mark.parametrize("offset", [0, 128, 256, 384, 64])
+def test_decode_pair_ranges_by_base(orc, cia, dev, offset):
+    """The decode's ranges per head pair follow the cache's base address: the
+    pair owning bytes 384..511 of each 512-byte block gets more workgroups.
+    The same 66 560-key cache at base offsets 0, 128, 256 and 384 bytes puts
+    that quarter on head pairs 3, 2, 1 and 0 in turn; a base 64 bytes off
+    (not 128-byte aligned) keeps equal ranges.  Each against the oracle."""
+    from cuda_inf_amd import kernels as K
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    ntok = 66560  # 1040 groups: two or more two-group units per FP8 wave
+    L = AttnLayer(ntok + 64, nsplit=16, device=dev)
+    ref = orc.Group64Cache(ntok + 64)
+    _, k, v = qkv(ntok, seed=ntok + offset, device="cpu", outliers=True)
+    _append(L, k, v, 0, dev)
+    ref.append(_u16(k), _u16(v), 0)
+    nb = L.kc8.numel()
+    kbuf = torch.zeros(nb + 1024, dtype=torch.uint8, device=dev)
+    vbuf = torch.zeros(nb + 1024, dtype=torch.uint8, device=dev)
+    base = (512 - kbuf.data_ptr() % 512) % 512 + offset
+    kc8 = kbuf[base:base + nb]
+    vbase = (512 - vbuf.data_ptr() % 512) % 512 + offset
+    vc8 = vbuf[vbase:vbase + nb]
+    kc8.copy_(L.kc8.reshape(-1))
+    vc8.copy_(L.vc8.reshape(-1))
+    assert kc8.data_ptr() % 512 == offset and vc8.data_ptr() % 512 == offset
+    qpos = ntok - 1
+    q, _, _ = qkv(1, seed=7 + offset, device="cpu", past=qpos)
+    out = torch.empty((32, 64), dtype=torch.float16, device=dev)
+    ws = torch.zeros(K.decode_workspace_bytes(qpos + 1), dtype=torch.uint8, device=dev)
+    K.attn_decode(q.to(dev), kc8, vc8, L.ksc, L.vsc, L.ktail, L.vtail, L.committed, qpos,
+                  0.125, out, ws)
+    torch.cuda.synchronize()
+    _, r32, _ = orc.attn_decode(_u16(q), ref, qpos, nsplit=16, nthreads=8)
+    assert_close_f16(_u16(out), r32)
+
+
 def test_split_combine_131k_tail(orc, cia, dev, cache131k):
     """The long-context shape of the split leg: 131072 committed keys and a
     9-key tail, 16 splits of 8193 keys (splits 0-14 each touch 129 groups,
