@@ -121,6 +121,35 @@ __global__ __launch_bounds__(kCombThreads) void k_decode_combine(const float* __
   }
 }
 
+// The same merge for up to kCombSmall splits: one wave per query head.
+// Lane s loads split s's m and l, lane d dim d of every split's o (all loads
+// out before any is used); the global max and the weights are per-lane work
+// over the splits, and each split's weight reaches the dims by readlane.
+// grid = 32 heads, block = 64.
+constexpr int kCombSmall = 32;
+__global__ __launch_bounds__(64) void k_decode_combine_small(const float* __restrict__ pm,
+                                                             const float* __restrict__ pl,
+                                                             const float* __restrict__ po,
+                                                             uint16_t* __restrict__ out,
+                                                             int nsplit) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const int ls = lane < nsplit ? lane : 0;
+  const float m = pm[(size_t)h * nsplit + ls], lv = pl[(size_t)h * nsplit + ls];
+  const float* ho = po + (size_t)h * nsplit * D + lane;
+  float ov[kCombSmall];
+#pragma unroll
+  for (int s = 0; s < kCombSmall; s++) ov[s] = ho[(size_t)(s < nsplit ? s : 0) * D];
+  const bool ok = lane < nsplit && lv > 0.f;  // (splits with l <= 0 are skipped)
+  const float M = wave_max_fast(ok ? m : -1e30f);
+  const float w = ok ? fast_exp(m - M) : 0.f;
+  const float L = wave_sum_fast(ok ? lv * w : 0.f);
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kCombSmall; s++)
+    acc = __builtin_fmaf(ov[s], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s)), acc);
+  out[h * D + lane] = f2h(acc / L);
+}
+
 }  // namespace cia
 
 using namespace cia;
@@ -170,8 +199,12 @@ extern "C" int cia_attn_decode_combine(const float* pm, const float* pl, const f
                                        uint16_t* out, int nsplit, void* stream) {
   CIA_REQUIRE(pm && pl && po && out, CIA_ERR_NULL);
   CIA_REQUIRE(nsplit >= 1 && nsplit <= CIA_NSPLIT_MAX, CIA_ERR_ARG);
-  hipLaunchKernelGGL(k_decode_combine, dim3(NH, D / kCombDims), dim3(kCombThreads), 0,
-                     (hipStream_t)stream, pm, pl, po, out, nsplit);
+  if (nsplit <= kCombSmall)
+    hipLaunchKernelGGL(k_decode_combine_small, dim3(NH), dim3(64), 0, (hipStream_t)stream, pm, pl,
+                       po, out, nsplit);
+  else
+    hipLaunchKernelGGL(k_decode_combine, dim3(NH, D / kCombDims), dim3(kCombThreads), 0,
+                       (hipStream_t)stream, pm, pl, po, out, nsplit);
   return launch_status();
 }
 

@@ -104,6 +104,8 @@ constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr int64_t kPartBytes = (int64_t)NKV * kMaxRanges * kPartF * sizeof(float);
 constexpr int64_t kWsBytes = kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
+// the split entry's workspace: two share slots per (kv head, range), then the counters
+constexpr int64_t kSplitWsBytes = 2 * kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
@@ -189,7 +191,8 @@ struct DecArgs {
   int nsplit, chunk, total;
   int sub;               // workgroups per split (> 1: each takes a share of one
                          // split and the last to arrive merges the shares,
-                         // through part and cnt[g * kCntStride + split])
+                         // through part and cnt[g * kCntStride + split]);
+                         // -1: range mode (the decode's ranges, rp / up)
 };
 
 // ---------------------------------------------------------------- kernel
@@ -207,7 +210,7 @@ struct DecArgs {
 // workgroup to arrive writes the split.  Keys outside a segment's range are
 // masked.  The tail keys (fp16 rows) of the splits a workgroup writes are
 // taken by its tail waves and folded in by the split's writer.
-template <bool kPrep, bool kSplit>
+template <bool kPrep, bool kSplit, bool kRange = false>
 __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
   uint16_t* sq = (uint16_t*)(lds + kLdsQ);
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   if (a.R == 1 || (kSplit && (a.R & 1))) {
     g = xcd;
     r = yy;
-  } else if (!kSplit && a.rp[0] > 0) {
+  } else if ((!kSplit || kRange) && a.rp[0] > 0) {
     // pair units: workgroups 16j + x and 16j + 8 + x (one XCD) take kv heads
     // 2p and 2p + 1 over the same range; XCD x holds units R/2 x .. R/2 x +
     // R/2 - 1 of the 4R, which go to the pairs in order, rp[p] each
@@ -245,7 +248,16 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // split mode: this workgroup's splits [s0, s0 + ns)
   int s0 = 0, ns = 0, sj = 0;
   if constexpr (kSplit) {
-    if (a.sub > 1) {
+    if constexpr (kRange) {
+      // range mode: the splits of the workgroup's committed groups [ga, gb),
+      // and for the last range a split of tail keys only, if there is one
+      const int ga = (int)(((unsigned)r * (unsigned)a.ng) / (unsigned)R);
+      const int gb = (int)(((unsigned)(r + 1) * (unsigned)a.ng) / (unsigned)R);
+      s0 = ga * G / a.chunk;
+      int shi = (gb * G - 1) / a.chunk;
+      if (r == R - 1) shi = max(shi, (a.total - 1) / a.chunk);
+      ns = shi - s0 + 1;
+    } else if (a.sub > 1) {
       s0 = r / a.sub;
       sj = r - s0 * a.sub;
       ns = 1;
@@ -285,8 +297,33 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     // part_i of its one split's groups (the split's waves are those w with
     // w ns / 8 equal)
     int sa = 0, sb = 0, part_i = 0, part_k = 1;
+    // range mode: the wave's keys in split s0 ([wa0, wa1)) and s0 + 1 ([wb0, wb1))
+    int wa0 = 0, wa1 = 0, wb0 = 0, wb1 = 0;
     if constexpr (kSplit) {
-      if (ns <= kFpWaves) {
+      if constexpr (kRange) {
+        // the workgroup's committed groups [ga, gb) as units per split
+        // segment (pairs from the segment's first group; a group holding the
+        // split boundary is in both segments), dealt to the 8 waves in order
+        const int ga = (int)(((unsigned)r * (unsigned)a.ng) / (unsigned)R);
+        const int gb = (int)(((unsigned)(r + 1) * (unsigned)a.ng) / (unsigned)R);
+        const int bnd = (s0 + 1) * a.chunk;           // first key of split s0 + 1
+        const int gA1 = min(gb, (bnd + G - 1) / G);   // segment A: groups [ga, gA1)
+        const int gB0 = bnd / G;                      // segment B: groups [gB0, gb)
+        const int uA = (gA1 - ga + 1) >> 1, uB = gB0 < gb ? (gb - gB0 + 1) >> 1 : 0;
+        const int U = uA + uB, u0 = w * U / kFpWaves, u1 = (w + 1) * U / kFpWaves;
+        wa0 = wa1 = wb0 = wb1 = 0;
+        if (u0 < min(u1, uA)) {
+          wa0 = (ga + 2 * u0) * G;
+          wa1 = min(ga + 2 * min(u1, uA), gA1) * G;
+        }
+        if (max(u0, uA) < u1) {
+          wb0 = (gB0 + 2 * (max(u0, uA) - uA)) * G;
+          wb1 = min(gB0 + 2 * (u1 - uA), gb) * G;
+        }
+        sa = wa0 < wa1 ? s0 : s0 + 1;
+        sb = wb0 < wb1 ? s0 + 2 : s0 + 1;
+        if (sa >= sb) sa = sb = s0;
+      } else if (ns <= kFpWaves) {
         const int j = (w * ns) / kFpWaves;
         const int fw = (j * kFpWaves + ns - 1) / ns, lw = ((j + 1) * kFpWaves + ns - 1) / ns;
         sa = s0 + j;
@@ -313,6 +350,10 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         const int q0 = G0 + part_i * ngr / part_k, q1 = G0 + (part_i + 1) * ngr / part_k;
         ka = max(a0, q0 * G);
         kb = min(b0, q1 * G);
+        if (ka >= kb) ka = kb = 0;
+      } else if constexpr (kRange) {
+        ka = max(a0, s > s0 ? wb0 : wa0);
+        kb = min(b0, s > s0 ? wb1 : wa1);
         if (ka >= kb) ka = kb = 0;
       } else {
         ka = a0;
@@ -431,6 +472,12 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS stores done (DMA still in flight)
     __builtin_amdgcn_s_barrier();        // B1: q rows in LDS
+    // range mode: the wave's partial of its first split (sml / sO) starts
+    // empty (l = 0; the merge skips empty partials), the second's is marked
+    // after the stream (f1: written)
+    bool f1 = false;
+    if constexpr (kSplit)
+      if (kRange && l < GQA) sml[w * GQA + l] = f32x2{-1e30f, 0.f};
     // B operand of S^T: lane (c, n = 4b + i) holds head i's dims when b == c
     f16x8 qop[8];
     {
@@ -596,7 +643,22 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         for (int d = 0; d < 4; d++)
 #pragma unroll
           for (int v = 0; v < 4; v++) Oc[d][v] = col4_sum(O[d][v]);
-        if (ns >= kFpWaves) {  // (then every split has one wave; else all go through the merge)
+        if (kRange && sp > s0) {
+          // range mode, the wave's second split (always its last): its
+          // partial into the wave's own K tile, free once the stream is done
+          float* x = (float*)(lds + kLdsK + (w & 7) * kHalfB);
+          if (l < 16) {
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+#pragma unroll
+              for (int v = 0; v < 4; v++) x[v * kPartRow + 4 + 16 * d + l] = Oc[d][v];
+          }
+          if (l < GQA) {
+            x[l * kPartRow] = mx;
+            x[l * kPartRow + 1] = lsum;
+          }
+          f1 = true;
+        } else if (ns >= kFpWaves) {  // (then every split has one wave; else all go through the merge)
           if (l < 16) {
 #pragma unroll
             for (int d = 0; d < 4; d++)
@@ -678,6 +740,13 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (a wave without units: its fetch done)
+    if constexpr (kSplit) {
+      if (kRange && !f1 && l < GQA) {
+        float* x = (float*)(lds + kLdsK + (w & 7) * kHalfB);
+        x[l * kPartRow] = -1e30f;
+        x[l * kPartRow + 1] = 0.f;
+      }
+    }
     if constexpr (!kSplit) {
       // ---- the four key blocks of each (head, dim) summed; lanes 0..15 hold
       // O[head v][16 delta + n]
@@ -897,6 +966,128 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       O = __builtin_fmaf(O, w0, ot * w1);
       M = Mn;
     };
+    if constexpr (kRange) {
+      // ---- range mode.  Threads jg = tid / 256 (head i, dim d) take the
+      // workgroup's splits s0 + jg and s0 + jg + 2 (the last range's split of
+      // tail keys only).  A split's writers are the ranges owning its first
+      // and last committed group (a split of tail keys only: the last range).
+      const int jg = tid >> 8, i = (tid >> 6) & 3, d = tid & 63, h = g * GQA + i;
+      auto owner = [&](int x) {  // the range holding committed group x
+        return (int)(((unsigned)(x + 1) * (unsigned)R + (unsigned)a.ng - 1) / (unsigned)a.ng) - 1;
+      };
+      auto writers = [&](int sp, int& rl, int& rh) {
+        const int k0 = sp * a.chunk, k1 = min(min(k0 + a.chunk, a.total), a.committed);
+        if (k0 >= k1) {
+          rl = rh = R - 1;
+          return;
+        }
+        rl = owner(k0 / G);
+        rh = owner((k1 - 1) / G);
+      };
+      auto write_split = [&](int sp, float M, float L, float O) {
+        const size_t pi = (size_t)h * a.nsplit + sp;
+        a.po[pi * D + d] = O;
+        if (d == 0) {
+          a.pm[pi] = L > 0.f ? M * kLn2 : -1e30f;
+          a.pl[pi] = L;
+        }
+      };
+      for (int j = jg; j < ns; j += 2) {
+        const int sp = s0 + j;
+        // the workgroup's share: its waves' partials in wave order (slot 0 in
+        // sml / sO, slot 1 in each wave's K tile; a split of tail keys only
+        // has none)
+        float M = -1e30f, L = 0.f, O = 0.f;
+        if (j < 2) {
+          for (int p = 0; p < kFpWaves; p++) {
+            float mp, lp, op;
+            if (j == 0) {
+              mp = sml[p * GQA + i][0];
+              lp = sml[p * GQA + i][1];
+              op = sO[(p * GQA + i) * D + d];
+            } else {
+              const float* x = (const float*)(lds + kLdsK + p * kHalfB) + i * kPartRow;
+              mp = x[0];
+              lp = x[1];
+              op = x[4 + d];
+            }
+            if (lp > 0.f) {
+              const float Mn = __builtin_fmaxf(M, mp);
+              const float c0 = L > 0.f ? __builtin_amdgcn_exp2f(M - Mn) : 0.f;
+              const float c1 = __builtin_amdgcn_exp2f(mp - Mn);
+              L = __builtin_fmaf(L, c0, lp * c1);
+              O = __builtin_fmaf(O, c0, op * c1);
+              M = Mn;
+            }
+          }
+        }
+        int rl, rh;
+        writers(sp, rl, rh);
+        if (rl == rh) {  // this workgroup's alone
+          if (sp >= tlo && sp <= thi) fold_tail(sp, i, d, M, L, O);
+          write_split(sp, M, L, O);
+        } else {
+          float* row = a.part + ((size_t)(g * 2 * kMaxRanges + 2 * r + j) * GQA + i) * kPartRow;
+          __hip_atomic_store(row + 4 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (d == 0) {
+            __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the shares have reached the agent
+      __builtin_amdgcn_s_barrier();        // the workgroup's shares stored
+      // a ticket per shared split: lane 0 of waves 0 and 1 (splits s0, s0 + 1)
+      uint32_t* sticket = (uint32_t*)(lds + kLdsTicket);
+      if (w < 2 && l == 0 && w < ns) {
+        int rl, rh;
+        writers(s0 + w, rl, rh);
+        if (rl != rh)
+          sticket[w] = __hip_atomic_fetch_add(a.cnt + g * kCntStride + s0 + w, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      if (jg < ns) {
+        const int j = jg, sp = s0 + j;
+        int rl, rh;
+        writers(sp, rl, rh);
+        if (rl == rh || sticket[j] != (uint32_t)(rh - rl)) return;
+        // ---- the last share of split sp to arrive: every share stored.  The
+        // counter goes back to zero for the next call.  Shares in range order.
+        if (i == 0 && d == 0)
+          __hip_atomic_store(a.cnt + g * kCntStride + sp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.part + (size_t)g * 2 * kMaxRanges * GQA * kPartRow);
+        float M = -1e30f, L = 0.f, O = 0.f;
+        for (int p0 = rl; p0 <= rh; p0 += 8) {
+          float mp[8], lp[8], op[8];
+#pragma unroll
+          for (int k = 0; k < 8; k++) {
+            const int rr = p0 + k <= rh ? p0 + k : p0;
+            const int ga = (int)(((unsigned)rr * (unsigned)a.ng) / (unsigned)R);
+            const int slot = 2 * rr + (sp - ga * G / a.chunk);
+            const int o = (slot * GQA + i) * kPartRow;
+            mp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, o * 4, 0, kCoherent));
+            lp[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + 1) * 4, 0, kCoherent));
+            op[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (o + 4 + d) * 4, 0, kCoherent));
+          }
+#pragma unroll
+          for (int k = 0; k < 8; k++) {
+            if (p0 + k <= rh && lp[k] > 0.f) {
+              const float Mn = __builtin_fmaxf(M, mp[k]);
+              const float c0 = L > 0.f ? __builtin_amdgcn_exp2f(M - Mn) : 0.f;
+              const float c1 = __builtin_amdgcn_exp2f(mp[k] - Mn);
+              L = __builtin_fmaf(L, c0, lp[k] * c1);
+              O = __builtin_fmaf(O, c0, op[k] * c1);
+              M = Mn;
+            }
+          }
+        }
+        if (sp >= tlo && sp <= thi) fold_tail(sp, i, d, M, L, O);
+        write_split(sp, M, L, O);
+      }
+      return;
+    }
     if (ns >= kFpWaves) {
       // the FP8 waves wrote their splits straight out (before B2): waves
       // 0-3 (head i = w, lane = dim) fold the tail into the tail splits
@@ -1280,13 +1471,13 @@ int split_ws_for_stream(void** out, hipStream_t s) {
   auto it = g_split_ws.find(key);
   if (it == g_split_ws.end()) {
     void* p = nullptr;
-    e = hipMalloc(&p, kWsBytes);
+    e = hipMalloc(&p, kSplitWsBytes);
     if (e != hipSuccess) {
       set_hip_error(e);
       return CIA_ERR_HIP;
     }
     hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, s,
-                       (uint32_t*)((char*)p + kPartBytes), NKV * kCntStride);
+                       (uint32_t*)((char*)p + 2 * kPartBytes), NKV * kCntStride);
     const int st = launch_status();
     if (st) {
       (void)hipFree(p);
@@ -1336,14 +1527,33 @@ extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
   int cap = kMaxRanges;
   const int cus = device_cus();
   if (cus > 0 && cus / NKV < cap) cap = cus / NKV > 0 ? cus / NKV : 1;
-  const int sub = nsplit < cap ? cap / nsplit : 1;
-  const int R = nsplit < cap ? nsplit * sub : cap;
+  int sub = nsplit < cap ? cap / nsplit : 1;
+  int R = nsplit < cap ? nsplit * sub : cap;
+  // Range mode, for fewer splits than workgroups when a split is at least
+  // as long as a workgroup's key range: the workgroups take the decode's
+  // key ranges of each kv head (unequal per head pair on long streams), a
+  // range touching at most two splits; a split's shares meet in part and
+  // the last workgroup to arrive writes it.
+  const int ng = committed / G;
+  DecArgs da{};
+  if (nsplit < cap && !(cap & 1) && ng >= cap) {
+    pair_ranges(ng, cap, slow_pair(kc8, vc8), da);
+    int rmin = cap;
+    if (da.rp[0] > 0)
+      for (int p = 0; p < 4; p++) rmin = std::min(rmin, da.rp[p]);
+    if ((int64_t)((ng + rmin - 1) / rmin) * G <= chunk) {
+      sub = -1;
+      R = cap;
+      for (int p = 0; p < 4; p++) da.nep[p] = 0;
+    } else {
+      da.rp[0] = 0;
+    }
+  }
   void* ws = nullptr;
-  if (sub > 1) {
+  if (sub > 1 || sub < 0) {
     const int st = split_ws_for_stream(&ws, (hipStream_t)stream);
     if (st) return st;
   }
-  DecArgs da{};
   da.q = q;
   da.kc8 = (uint8_t*)kc8;
   da.vc8 = (uint8_t*)vc8;
@@ -1364,8 +1574,11 @@ extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
   da.total = total;
   da.sub = sub;
   da.part = (float*)ws;
-  da.cnt = ws ? (uint32_t*)((char*)ws + kPartBytes) : nullptr;
+  da.cnt = ws ? (uint32_t*)((char*)ws + 2 * kPartBytes) : nullptr;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((k_decode<false, true>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+  if (sub < 0)
+    hipLaunchKernelGGL((k_decode<false, true, true>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
+  else
+    hipLaunchKernelGGL((k_decode<false, true>), dim3(NKV * R), dim3(kDecThreads), 0, s, da);
   return launch_status();
 }
