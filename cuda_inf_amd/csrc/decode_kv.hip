@@ -1452,8 +1452,9 @@ int scratch_for_device(void** out, hipStream_t s) {
   return CIA_OK;
 }
 
-// The split entry's share workspace (the layout of cia_attn_decode's), one
-// per (device, stream): allocated and its counters cleared on the first call
+// The split entry's share workspace (kSplitWsBytes: two share slots per
+// (kv head, range), then the counters), one per (device, stream):
+// allocated and its counters cleared on the first call
 // on a stream, kept until the process ends.  Calls on one stream run in
 // order, and calls on different streams use different workspaces.
 std::mutex g_split_mu;

@@ -135,7 +135,7 @@ int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
  * (the reference fixes 16).  With fewer splits than the launch has
  * workgroups per kv head, each split is shared by several workgroups that
  * meet in a device workspace the library allocates on the first call on a
- * stream (per device and stream, about 380 KB, kept until the process
+ * stream (per device and stream, 750 KiB, kept until the process
  * ends): that first call is not capturable into a graph. */
 int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
                           const uint8_t* vc8, const uint16_t* ksc,
