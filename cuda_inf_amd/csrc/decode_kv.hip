@@ -207,7 +207,11 @@ struct DecArgs {
 // 8 splits or more (one wave per split), else through LDS and its merge.
 // With sub > 1 workgroups per split (fewer splits than ranges), workgroup r
 // takes share r % sub of split r / sub; the shares meet in part and the last
-// workgroup to arrive writes the split.  Keys outside a segment's range are
+// workgroup to arrive writes the split.  kRange (fewer splits than ranges,
+// each split at least as long as a range): the workgroups take the
+// decode's key ranges (rp / up), each touching at most two splits, and a
+// split's shares (one per range touching it) meet in part, the last range
+// to arrive writing the split.  Keys outside a segment's range are
 // masked.  The tail keys (fp16 rows) of the splits a workgroup writes are
 // taken by its tail waves and folded in by the split's writer.
 template <bool kPrep, bool kSplit, bool kRange = false>
