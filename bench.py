@@ -66,6 +66,8 @@ def main():
                          "projections, producers, attention, out_proj + residual (0 = skip)")
     ap.add_argument("--h2o-steps", type=int, default=4000,
                     help="H2O decode steps after a 1024-token prompt (0 = skip)")
+    ap.add_argument("--upload-mib", type=int, default=1024,
+                    help="weights.bin upload leg: MiB of synthetic file (0 = skip)")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="MiB: first run a plain device copy of this size three times "
                          "(the reference dispatch that scales rocprofv3 byte counters)")
@@ -453,6 +455,9 @@ def main():
     # ---- H2O leg: 2048-slot buffer, window 256, 1024-token prompt
     h2o = h2o_leg(a.h2o_steps, dev, stream, log) if a.h2o_steps > 0 else None
 
+    # ---- weights.bin upload: pinned double-buffered against one pageable buffer
+    upload = upload_leg(a.upload_mib, dev, log) if a.upload_mib > 0 else None
+
     # ---- CPU baseline: the oracle on this host's cores, one layer at a time
     cpu = None
     if not a.no_cpu:
@@ -511,9 +516,65 @@ def main():
         "attention_branch": block,
         "long_context": long_ctx,
         "h2o": h2o,
+        "weights_upload": upload,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+
+def upload_leg(mib, dev, log, runs=3):
+    """weights.bin into HBM (engine.cu:678-692): cia_weights_upload (12
+    reader threads, two pinned 64 MiB buffers, each copy overlapping the
+    next reads) against the reference's scheme (one pageable 256 MiB
+    buffer: read, then a blocking copy).  The synthetic file was just
+    written, so both read it from the page cache: host memory to HBM."""
+    import tempfile
+    import numpy as np
+    import torch
+    from cuda_inf_amd.model_files import upload_file
+    nbytes = mib << 20
+    d = tempfile.mkdtemp(prefix="cia_upload_")
+    path = os.path.join(d, "weights.bin")
+    try:
+        block = np.random.default_rng(1).integers(0, 256, 64 << 20, dtype=np.uint8)
+        with open(path, "wb") as f:
+            for off in range(0, nbytes, block.size):
+                f.write(block[:min(block.size, nbytes - off)].tobytes())
+        blob = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ours, theirs = [], []
+        buf = np.empty(256 << 20, np.uint8)
+        for _ in range(runs):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            upload_file(path, blob)
+            ours.append(time.perf_counter() - t0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with open(path, "rb", buffering=0) as f:
+                off = 0
+                while off < nbytes:
+                    r = f.readinto(memoryview(buf)[:min(buf.size, nbytes - off)])
+                    blob[off:off + r].copy_(torch.from_numpy(buf[:r]))
+                    off += r
+            torch.cuda.synchronize()
+            theirs.append(time.perf_counter() - t0)
+        # (the last copy wrote the file's bytes; check the tail chunk)
+        tail = min(nbytes, 1 << 20)
+        assert torch.equal(blob[nbytes - tail:].cpu(),
+                           torch.from_numpy(np.fromfile(path, np.uint8, tail, offset=nbytes - tail)))
+    finally:
+        try:
+            os.remove(path)
+        except OSError:
+            pass
+        os.rmdir(d)
+    o, t = float(np.median(ours)), float(np.median(theirs))
+    log(f"weights upload {mib} MiB: {nbytes / o / 1e9:.1f} GB/s pinned double-buffered "
+        f"({o * 1e3:.0f} ms); one pageable 256 MiB buffer {nbytes / t / 1e9:.1f} GB/s "
+        f"({t * 1e3:.0f} ms)")
+    return {"mib": mib, "gbps": round(nbytes / o / 1e9, 2), "ms": round(o * 1e3, 1),
+            "pageable_256mib_gbps": round(nbytes / t / 1e9, 2),
+            "source": "page cache (file just written)"}
 
 
 def long_context_leg(ctx, nL, steps, dev, stream, log):

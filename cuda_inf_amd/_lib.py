@@ -21,7 +21,8 @@ HIDDEN = 2048  # hidden size H (engine.cu:33)
 NSPLIT_MAX = 4096
 
 STATUS = {0: "CIA_OK", 1: "CIA_ERR_NULL", 2: "CIA_ERR_ALIGN", 3: "CIA_ERR_ARG",
-          4: "CIA_ERR_HIP", 5: "CIA_ERR_STATE", 6: "CIA_ERR_NOSLOT"}
+          4: "CIA_ERR_HIP", 5: "CIA_ERR_STATE", 6: "CIA_ERR_NOSLOT",
+          7: "CIA_ERR_IO"}
 
 # Every symbol include/cuda_inf_attn.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -59,6 +60,14 @@ SIGNATURES = {
     "cia_layer_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
     "cia_layer_append": (_I, [_P, _P, _P, _I, _I, _P]),
     "cia_decode_loop": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
+    # include/cuda_inf_model.h
+    "cia_index_read": (_I, [ctypes.c_char_p, _P, ctypes.c_int64, _P]),
+    "cia_file_size": (_I, [ctypes.c_char_p, _P]),
+    "cia_weights_upload": (_I, [ctypes.c_char_p, _P, ctypes.c_uint64, _P, _P]),
+    "cia_tok_load": (_I, [ctypes.c_char_p, _P]),
+    "cia_tok_free": (None, [_P]),
+    "cia_tok_encode": (_I, [_P, ctypes.c_char_p, ctypes.c_int64, _P, ctypes.c_int64, _P]),
+    "cia_tok_decode": (_I, [_P, _P, ctypes.c_int64, _I, _P, ctypes.c_int64, _P]),
 }
 
 
@@ -108,6 +117,13 @@ def check(fn: str, code: int) -> None:
 
 def call(fn: str, *args) -> None:
     check(fn, getattr(lib(), fn)(*args))
+
+
+class cia_tensor_desc(ctypes.Structure):
+    """Mirror of ``cia_tensor_desc`` in include/cuda_inf_model.h."""
+    _fields_ = [("name", ctypes.c_char * 256), ("kind", ctypes.c_int32),
+                ("offset", ctypes.c_uint64), ("packed", ctypes.c_uint64),
+                ("scales", ctypes.c_uint64), ("d0", ctypes.c_int64), ("d1", ctypes.c_int64)]
 
 
 class cia_append_op(ctypes.Structure):

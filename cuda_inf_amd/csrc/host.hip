@@ -70,6 +70,7 @@ extern "C" const char* cia_strerror(int status) {
     case CIA_ERR_HIP: return "HIP runtime call or kernel launch failed";
     case CIA_ERR_STATE: return "cache state inconsistent (tail would exceed 64 tokens)";
     case CIA_ERR_NOSLOT: return "H2O: no slot below 1e30 could be evicted";
+    case CIA_ERR_IO: return "model file could not be opened, read or parsed";
     default: return "unknown status";
   }
 }

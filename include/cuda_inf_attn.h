@@ -62,7 +62,9 @@ typedef enum cia_status {
   CIA_ERR_ARG = 3,        /* an integer argument is out of range */
   CIA_ERR_HIP = 4,        /* a HIP runtime call or launch failed */
   CIA_ERR_STATE = 5,      /* host-side cache state is inconsistent */
-  CIA_ERR_NOSLOT = 6      /* H2O: no slot could be chosen for eviction */
+  CIA_ERR_NOSLOT = 6,     /* H2O: no slot could be chosen for eviction */
+  CIA_ERR_IO = 7          /* a model file could not be opened, read or parsed
+                             (include/cuda_inf_model.h) */
 } cia_status;
 
 const char* cia_strerror(int status);

@@ -10,11 +10,11 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "cuda_inf_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("cuda_inf_attn.h", "cuda_inf_model.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(cia_[a-z0-9_]+)\s*\(", text)))
 
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(cia):
 def test_status_strings(cia):
     from cuda_inf_amd import _lib
     L = _lib.lib()
-    for code in range(7):
+    for code in range(8):
         assert L.cia_strerror(code) and L.cia_strerror(code) != b"unknown status"
     assert L.cia_strerror(99) == b"unknown status"
 
