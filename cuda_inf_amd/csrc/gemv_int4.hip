@@ -135,6 +135,19 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv_int4(GemvArgs a) {
   const int c0 = l < nch ? l : nch - 1;
   u32x4 wv = *(const u32x4*)(wp + 16 * c0);
   uint32_t sv = sp[c0 >> 2];  // (32-bit holder: no early wait)
+  float* y32 = mi == 0 ? a.mat[0].y32 : (mi == 1 ? a.mat[1].y32 : a.mat[2].y32);
+  uint16_t* y16 = mi == 0 ? a.mat[0].y16 : (mi == 1 ? a.mat[1].y16 : a.mat[2].y16);
+  const int N = mi == 0 ? a.mat[0].N : (mi == 1 ? a.mat[1].N : a.mat[2].N);
+  // the residual (add): fetched with the weights, so the epilogue does not
+  // wait a round trip for it (the wave's lanes share the address; without
+  // add, a harmless read of x[0])
+  float yold[kM];
+#pragma unroll
+  for (int m = 0; m < kM; m++) {
+    const int mm = m0 + m < a.M ? m0 + m : a.M - 1;
+    const float* ysrc = a.add && y32 ? y32 + (size_t)mm * N + n : (const float*)a.x;
+    yold[m] = *ysrc;
+  }
   if constexpr (kStage > 0) {
 #pragma unroll
     for (int i = 0; i < kStage; i++) {
@@ -169,15 +182,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv_int4(GemvArgs a) {
       acc[m] = __builtin_fmaf(chunk_dot(wv, p), h2f((uint16_t)sv), acc[m]);
     }
   }
-  float* y32 = mi == 0 ? a.mat[0].y32 : (mi == 1 ? a.mat[1].y32 : a.mat[2].y32);
-  uint16_t* y16 = mi == 0 ? a.mat[0].y16 : (mi == 1 ? a.mat[1].y16 : a.mat[2].y16);
-  const int N = mi == 0 ? a.mat[0].N : (mi == 1 ? a.mat[1].N : a.mat[2].N);
 #pragma unroll
   for (int m = 0; m < kM; m++) {
     const float v = wave_sum_fast(acc[m]);
     if (l == 0 && row < a.rows && m0 + m < a.M) {
       const size_t o = (size_t)(m0 + m) * N + n;
-      if (y32) y32[o] = a.add ? y32[o] + v : v;
+      if (y32) y32[o] = a.add ? yold[m] + v : v;
       if (y16) y16[o] = f2h(v);
     }
   }
