@@ -12,7 +12,12 @@ Pinned by tests/test_oracle_model_files.py:
     differ (a tab before letters; non-ASCII punctuation counted as a letter).
   - encode / decode: the HuggingFace `tokenizers` library (BPE with
     ignore_merges, the same split pattern, byte-level mapping) on a
-    tokenizer trained from synthetic text; decode(encode(s)) == s.
+    tokenizer trained from synthetic text; decode(encode(s)) == s;
+  - and, where the reference tree is present, src/tokenizer.h itself:
+    oracle/Makefile compiles the header where it lies (with ref_tok.cpp, a
+    C-ABI shim) into oracle/_ref/libreftok.so, and ``RefTokenizer`` calls
+    it; encode and decode agree on the golden cases, random text and bytes,
+    random ids and degenerate files.
 """
 from __future__ import annotations
 
@@ -331,3 +336,59 @@ class Tokenizer:
             if 0 <= i < len(self.id2tok):
                 bl += self.id2tok[i]
         return out + self._bl_to_raw(bl)
+
+
+# ------------------------------------------------ the reference's tokenizer
+
+REF_TOK_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_ref", "libreftok.so")
+
+
+class RefTokenizer:
+    """src/tokenizer.h itself, compiled by oracle/Makefile into
+    oracle/_ref/libreftok.so (present only where the reference tree was
+    available at build time; ``available()`` says so)."""
+
+    _lib = None
+
+    @classmethod
+    def available(cls) -> bool:
+        return os.path.exists(REF_TOK_LIB)
+
+    @classmethod
+    def _l(cls):
+        import ctypes
+        if cls._lib is None:
+            L = ctypes.CDLL(REF_TOK_LIB)
+            P, I64 = ctypes.c_void_p, ctypes.c_int64
+            L.ref_tok_load.restype, L.ref_tok_load.argtypes = P, [ctypes.c_char_p]
+            L.ref_tok_free.restype, L.ref_tok_free.argtypes = None, [P]
+            L.ref_tok_encode.restype = I64
+            L.ref_tok_encode.argtypes = [P, ctypes.c_char_p, I64, P, I64]
+            L.ref_tok_decode.restype = I64
+            L.ref_tok_decode.argtypes = [P, P, I64, ctypes.c_int, P, I64]
+            cls._lib = L
+        return cls._lib
+
+    def __init__(self, d: str):
+        self.h = self._l().ref_tok_load(os.fsencode(d))
+        if not self.h:
+            raise FileNotFoundError(d)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self._l().ref_tok_free(self.h)
+
+    def encode(self, text: bytes) -> list[int]:
+        import ctypes
+        buf = (ctypes.c_int32 * max(len(text), 1))()
+        n = self._l().ref_tok_encode(self.h, text, len(text), buf, len(text))
+        return list(buf[:n])
+
+    def decode(self, ids, skip_special: bool = False) -> bytes:
+        import ctypes
+        ids = list(ids)
+        arr = (ctypes.c_int32 * max(len(ids), 1))(*ids)
+        n = self._l().ref_tok_decode(self.h, arr, len(ids), int(skip_special), None, 0)
+        out = ctypes.create_string_buffer(max(n, 1))
+        self._l().ref_tok_decode(self.h, arr, len(ids), int(skip_special), out, n)
+        return out.raw[:n]

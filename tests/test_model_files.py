@@ -62,6 +62,24 @@ def test_random_bytes_match_oracle(toks):
         assert t.encode(b) == ref.encode(b), b
 
 
+@pytest.mark.skipif(not om.RefTokenizer.available(),
+                    reason="oracle/_ref/libreftok.so not built (no reference tree)")
+def test_matches_compiled_reference_tokenizer(toks):
+    """Directly against src/tokenizer.h compiled from the header."""
+    t, _ = toks
+    ref = om.RefTokenizer(TOK)
+    rng = random.Random(24)
+    pool = [chr(c) for c in range(32, 127)] * 3 + list("\t\n\r\xa0éß中€\U0001F600́")
+    for _ in range(300):
+        if rng.random() < 0.3:
+            b = bytes(rng.randrange(256) for _ in range(rng.randint(0, 64)))
+        else:
+            b = "".join(rng.choice(pool) for _ in range(rng.randint(0, 100))).encode()
+        ids = t.encode(b)
+        assert ids == ref.encode(b), b
+        assert t.decode_bytes(ids) == ref.decode(ids)
+
+
 def test_decode_random_ids(toks):
     t, ref = toks
     rng = random.Random(23)

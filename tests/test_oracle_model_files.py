@@ -106,3 +106,71 @@ def test_oracle_round_trip_and_specials():
     assert tok.encode(b"<think></think>") == [sp[b"<think></think>"]]
     assert tok.encode(b"<think></thin")[0] == sp[b"<think>"]
     assert tok.decode([sp[b"<|im_end|>"], 999999, -1], skip_special=True) == b""
+
+
+ref_tok = pytest.mark.skipif(not om.RefTokenizer.available(),
+                             reason="oracle/_ref/libreftok.so not built (no reference tree)")
+
+
+def _random_inputs(seed, n):
+    rng = random.Random(seed)
+    pool = ([chr(c) for c in range(32, 127)] * 3 + list("\t\n\r\x0b\x0c\xa0") +
+            list("éßñ中文ми€\U0001F600́　 ٣"))
+    out = []
+    for _ in range(n):
+        if rng.random() < 0.25:
+            out.append(bytes(rng.randrange(256) for _ in range(rng.randint(0, 64))))
+        else:
+            out.append("".join(rng.choice(pool) for _ in range(rng.randint(0, 120))).encode())
+    return out
+
+
+@ref_tok
+def test_oracle_matches_compiled_reference_tokenizer():
+    """The oracle against src/tokenizer.h itself (compiled from the header
+    where it lies): golden cases, random UTF-8 and random bytes, specials
+    inserted, decode of random ids with and without skip_special."""
+    d = os.path.join(GOLD, "tok")
+    ref, tok = om.RefTokenizer(d), om.Tokenizer.load(d)
+    cases = json.load(open(os.path.join(GOLD, "tok_cases.json"), encoding="utf-8"))["cases"]
+    texts = [c["text"].encode() for c in cases] + _random_inputs(41, 500)
+    specials = [c for c, _ in tok.specials]
+    rng = random.Random(42)
+    for t in texts:
+        if rng.random() < 0.3:
+            k = rng.randint(0, len(t))
+            t = t[:k] + rng.choice(specials) + t[k:]
+        assert tok.encode(t) == ref.encode(t), t
+    nv = len(tok.id2tok)
+    for _ in range(300):
+        ids = [rng.randrange(-3, nv + 5) for _ in range(rng.randint(0, 40))]
+        for skip in (False, True):
+            assert tok.decode(ids, skip) == ref.decode(ids, skip), ids
+
+
+@ref_tok
+def test_oracle_matches_compiled_reference_on_degenerate_files(tmp_path):
+    """Merge results missing from the vocabulary, duplicate lines, a tab
+    inside B, lines without a tab.  Left out, as undefined in the reference:
+    an empty special (its encode would loop forever) and a negative id (its
+    load writes before the id table)."""
+    tab = om.byte_table()
+    vocab = [b"%d\t%s" % (i, tab[b].encode()) for i, b in enumerate(range(256))]
+    vocab += [b"256\tab", b"257\tabc", b"258\txyz", b"259\tab", b"no tab line", b"260\tneg"]
+    merges = [b"0\ta\tb", b"1\tab\tc", b"2\tx\ty", b"3\txy\tz", b"5\tq\tq", b"4\tc\td",
+              b"7\tab\tcd", b"9\tz\tz\tz", b"x", b"6\tq\tq"]
+    special = [b"300\t<s>", b"302\t<s>x", b"bad"]
+    d = tmp_path / "tok"
+    d.mkdir()
+    for name, lines in (("vocab.tsv", vocab), ("merges.tsv", merges), ("special.tsv", special)):
+        (d / name).write_bytes(b"".join(x + b"\n" for x in lines))
+    ref, tok = om.RefTokenizer(str(d)), om.Tokenizer.load(str(d))
+    rng = random.Random(7)
+    for s in [b"abc", b"abcd", b"xyz", b"xyzz", b"qqq", b"qqqq", b"cdab", b"<s>x<s><s>y",
+              b"zzz", b"ab ab", b"neg"] + [
+            bytes(rng.choice(b"abcdxyzq <s>") for _ in range(rng.randint(0, 30)))
+            for _ in range(300)]:
+        assert tok.encode(s) == ref.encode(s), s
+    ids = list(range(-2, 310))
+    assert tok.decode(ids) == ref.decode(ids)
+    assert tok.decode(ids, True) == ref.decode(ids, True)
