@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cerrno>
 #include <climits>
+#include <memory>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -76,13 +77,18 @@ bool read_parallel(int fd, uint8_t* dst, uint64_t off, uint64_t len) {
       1, std::min<uint64_t>(std::min<uint64_t>(kReaders, hw), len / kSlice));
   const uint64_t per = (len + nt - 1) / nt;
   bool ok[kReaders];
-  std::vector<std::thread> th;
+  std::thread th[kReaders];
   for (int t = 1; t < nt; t++) {
     const uint64_t a = std::min(len, t * per), b = std::min(len, (t + 1) * per);
-    th.emplace_back([=, &ok] { ok[t] = pread_all(fd, dst + a, off + a, b - a); });
+    try {
+      th[t] = std::thread([=, &ok] { ok[t] = pread_all(fd, dst + a, off + a, b - a); });
+    } catch (...) {  // (no thread to be had: this slice on the calling thread)
+      ok[t] = pread_all(fd, dst + a, off + a, b - a);
+    }
   }
   ok[0] = pread_all(fd, dst, off, std::min(len, per));
-  for (auto& x : th) x.join();
+  for (int t = 1; t < nt; t++)
+    if (th[t].joinable()) th[t].join();
   for (int t = 0; t < nt; t++)
     if (!ok[t]) return false;
   return true;
@@ -210,6 +216,17 @@ void pieces(const std::vector<uint32_t>& c, std::vector<int>& ends) {
 struct Merge {
   int32_t rank, out;  // out: symbol index of the merged string
 };
+
+// No C++ exception crosses the C ABI: a failed allocation while reading a
+// file or tokenizing becomes CIA_ERR_IO.
+template <typename F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (...) {
+    return CIA_ERR_IO;
+  }
+}
 
 }  // namespace
 
@@ -367,32 +384,34 @@ bool tsv_lines(const std::string& path, std::vector<std::string>& lines) {
 
 extern "C" int cia_index_read(const char* path, cia_tensor_desc* out, int64_t cap,
                               int64_t* count) {
-  if (!path || !count) return CIA_ERR_NULL;
-  std::string s;
-  if (!read_file(path, s)) return CIA_ERR_IO;
-  size_t p = 0;
-  uint32_t nt;
-  if (!take(s, p, nt)) return CIA_ERR_IO;
-  if (out && cap < (int64_t)nt) {
+  return guarded([&]() -> int {
+    if (!path || !count) return CIA_ERR_NULL;
+    std::string s;
+    if (!read_file(path, s)) return CIA_ERR_IO;
+    size_t p = 0;
+    uint32_t nt;
+    if (!take(s, p, nt)) return CIA_ERR_IO;
+    if (out && cap < (int64_t)nt) {
+      *count = nt;
+      return CIA_ERR_ARG;
+    }
+    for (uint32_t i = 0; i < nt; i++) {
+      uint8_t nl, kind;
+      cia_tensor_desc d;
+      memset(&d, 0, sizeof d);
+      if (!take(s, p, nl) || s.size() - p < nl) return CIA_ERR_IO;
+      memcpy(d.name, s.data() + p, nl);
+      p += nl;
+      if (!take(s, p, kind) || kind > 1 || !take(s, p, d.offset) || !take(s, p, d.packed) ||
+          !take(s, p, d.scales) || !take(s, p, d.d0) || !take(s, p, d.d1))
+        return CIA_ERR_IO;
+      d.kind = kind;
+      if (out) out[i] = d;
+    }
+    if (p != s.size()) return CIA_ERR_IO;
     *count = nt;
-    return CIA_ERR_ARG;
-  }
-  for (uint32_t i = 0; i < nt; i++) {
-    uint8_t nl, kind;
-    cia_tensor_desc d;
-    memset(&d, 0, sizeof d);
-    if (!take(s, p, nl) || s.size() - p < nl) return CIA_ERR_IO;
-    memcpy(d.name, s.data() + p, nl);
-    p += nl;
-    if (!take(s, p, kind) || kind > 1 || !take(s, p, d.offset) || !take(s, p, d.packed) ||
-        !take(s, p, d.scales) || !take(s, p, d.d0) || !take(s, p, d.d1))
-      return CIA_ERR_IO;
-    d.kind = kind;
-    if (out) out[i] = d;
-  }
-  if (p != s.size()) return CIA_ERR_IO;
-  *count = nt;
-  return CIA_OK;
+    return CIA_OK;
+  });
 }
 
 extern "C" int cia_file_size(const char* path, uint64_t* bytes) {
@@ -459,82 +478,88 @@ extern "C" int cia_weights_upload(const char* path, void* dst, uint64_t cap, uin
 }
 
 extern "C" int cia_tok_load(const char* dir, cia_tokenizer** out) {
-  if (!dir || !out) return CIA_ERR_NULL;
-  *out = nullptr;
-  const std::string d(dir);
-  std::vector<std::string> voc, mer, spe;
-  if (!tsv_lines(d + "/vocab.tsv", voc) || !tsv_lines(d + "/merges.tsv", mer) ||
-      !tsv_lines(d + "/special.tsv", spe))
-    return CIA_ERR_IO;
-  auto* t = new cia_tokenizer();
-  t->byte_table();
-  for (int b = 0; b < 256; b++) t->intern(t->byte_char[b]);
-  // vocabulary "<id>\t<token>": a later line for the same token or id wins
-  int32_t maxid = 0;
-  std::vector<std::pair<int32_t, std::string>> ent;
-  for (const auto& ln : voc) {
-    const size_t tab = ln.find('\t');
-    if (tab == std::string::npos) continue;
-    const int32_t id = (int32_t)atoi(ln.substr(0, tab).c_str());
-    ent.emplace_back(id, ln.substr(tab + 1));
-    t->vid[(size_t)t->intern(ent.back().second)] = id;
-    maxid = std::max(maxid, id);
-  }
-  t->id_str.assign((size_t)maxid + 1, std::string());
-  for (const auto& e : ent)
-    if (e.first >= 0) t->id_str[(size_t)e.first] = e.second;
-  // merges "<rank>\t<A>\t<B>"
-  for (const auto& ln : mer) {
-    const size_t t1 = ln.find('\t');
-    if (t1 == std::string::npos) continue;
-    const size_t t2 = ln.find('\t', t1 + 1);
-    if (t2 == std::string::npos) continue;
-    const std::string a = ln.substr(t1 + 1, t2 - t1 - 1), b = ln.substr(t2 + 1);
-    const int32_t rank = (int32_t)atoi(ln.substr(0, t1).c_str());
-    const int32_t ia = t->intern(a), ib = t->intern(b), iab = t->intern(a + b);
-    t->merges[(uint64_t)(uint32_t)ia << 32 | (uint32_t)ib] = Merge{rank, iab};
-  }
-  // special tokens "<id>\t<content>"
-  std::vector<std::pair<std::string, int32_t>> sp;
-  for (const auto& ln : spe) {
-    const size_t tab = ln.find('\t');
-    if (tab == std::string::npos) continue;
-    const int32_t id = (int32_t)atoi(ln.substr(0, tab).c_str());
-    std::string c = ln.substr(tab + 1);
-    t->special_str[id] = c;
-    if (!c.empty()) sp.emplace_back(std::move(c), id);
-  }
-  std::stable_sort(sp.begin(), sp.end(),
-                   [](const auto& x, const auto& y) { return x.first.size() > y.first.size(); });
-  for (auto& x : sp) t->special_by_byte[(unsigned char)x.first[0]].push_back(x);
-  *out = t;
-  return CIA_OK;
+  return guarded([&]() -> int {
+    if (!dir || !out) return CIA_ERR_NULL;
+    *out = nullptr;
+    const std::string d(dir);
+    std::vector<std::string> voc, mer, spe;
+    if (!tsv_lines(d + "/vocab.tsv", voc) || !tsv_lines(d + "/merges.tsv", mer) ||
+        !tsv_lines(d + "/special.tsv", spe))
+      return CIA_ERR_IO;
+    std::unique_ptr<cia_tokenizer> t(new cia_tokenizer());
+    t->byte_table();
+    for (int b = 0; b < 256; b++) t->intern(t->byte_char[b]);
+    // vocabulary "<id>\t<token>": a later line for the same token or id wins
+    int32_t maxid = 0;
+    std::vector<std::pair<int32_t, std::string>> ent;
+    for (const auto& ln : voc) {
+      const size_t tab = ln.find('\t');
+      if (tab == std::string::npos) continue;
+      const int32_t id = (int32_t)atoi(ln.substr(0, tab).c_str());
+      ent.emplace_back(id, ln.substr(tab + 1));
+      t->vid[(size_t)t->intern(ent.back().second)] = id;
+      maxid = std::max(maxid, id);
+    }
+    t->id_str.assign((size_t)maxid + 1, std::string());
+    for (const auto& e : ent)
+      if (e.first >= 0) t->id_str[(size_t)e.first] = e.second;
+    // merges "<rank>\t<A>\t<B>"
+    for (const auto& ln : mer) {
+      const size_t t1 = ln.find('\t');
+      if (t1 == std::string::npos) continue;
+      const size_t t2 = ln.find('\t', t1 + 1);
+      if (t2 == std::string::npos) continue;
+      const std::string a = ln.substr(t1 + 1, t2 - t1 - 1), b = ln.substr(t2 + 1);
+      const int32_t rank = (int32_t)atoi(ln.substr(0, t1).c_str());
+      const int32_t ia = t->intern(a), ib = t->intern(b), iab = t->intern(a + b);
+      t->merges[(uint64_t)(uint32_t)ia << 32 | (uint32_t)ib] = Merge{rank, iab};
+    }
+    // special tokens "<id>\t<content>"
+    std::vector<std::pair<std::string, int32_t>> sp;
+    for (const auto& ln : spe) {
+      const size_t tab = ln.find('\t');
+      if (tab == std::string::npos) continue;
+      const int32_t id = (int32_t)atoi(ln.substr(0, tab).c_str());
+      std::string c = ln.substr(tab + 1);
+      t->special_str[id] = c;
+      if (!c.empty()) sp.emplace_back(std::move(c), id);
+    }
+    std::stable_sort(sp.begin(), sp.end(),
+                     [](const auto& x, const auto& y) { return x.first.size() > y.first.size(); });
+    for (auto& x : sp) t->special_by_byte[(unsigned char)x.first[0]].push_back(x);
+    *out = t.release();
+    return CIA_OK;
+  });
 }
 
 extern "C" void cia_tok_free(cia_tokenizer* tok) { delete tok; }
 
 extern "C" int cia_tok_encode(const cia_tokenizer* tok, const char* text, int64_t len,
                               int32_t* ids, int64_t cap, int64_t* n) {
-  if (!tok || !n || (!text && len > 0)) return CIA_ERR_NULL;
-  if (len < 0) return CIA_ERR_ARG;
-  std::vector<int32_t> v;
-  tok->encode(text, (size_t)len, v);
-  *n = (int64_t)v.size();
-  if (!ids) return CIA_OK;
-  if (cap < (int64_t)v.size()) return CIA_ERR_ARG;
-  if (!v.empty()) memcpy(ids, v.data(), v.size() * sizeof(int32_t));
-  return CIA_OK;
+  return guarded([&]() -> int {
+    if (!tok || !n || (!text && len > 0)) return CIA_ERR_NULL;
+    if (len < 0) return CIA_ERR_ARG;
+    std::vector<int32_t> v;
+    tok->encode(text, (size_t)len, v);
+    *n = (int64_t)v.size();
+    if (!ids) return CIA_OK;
+    if (cap < (int64_t)v.size()) return CIA_ERR_ARG;
+    if (!v.empty()) memcpy(ids, v.data(), v.size() * sizeof(int32_t));
+    return CIA_OK;
+  });
 }
 
 extern "C" int cia_tok_decode(const cia_tokenizer* tok, const int32_t* ids, int64_t n,
                               int skip_special, char* out, int64_t cap, int64_t* len) {
-  if (!tok || !len || (!ids && n > 0)) return CIA_ERR_NULL;
-  if (n < 0) return CIA_ERR_ARG;
-  std::string s;
-  tok->decode(ids, n, skip_special != 0, s);
-  *len = (int64_t)s.size();
-  if (!out) return CIA_OK;
-  if (cap < (int64_t)s.size()) return CIA_ERR_ARG;
-  if (!s.empty()) memcpy(out, s.data(), s.size());
-  return CIA_OK;
+  return guarded([&]() -> int {
+    if (!tok || !len || (!ids && n > 0)) return CIA_ERR_NULL;
+    if (n < 0) return CIA_ERR_ARG;
+    std::string s;
+    tok->decode(ids, n, skip_special != 0, s);
+    *len = (int64_t)s.size();
+    if (!out) return CIA_OK;
+    if (cap < (int64_t)s.size()) return CIA_ERR_ARG;
+    if (!s.empty()) memcpy(out, s.data(), s.size());
+    return CIA_OK;
+  });
 }
