@@ -29,8 +29,9 @@
 //             are the B operand as they stand; V^T slots are ordered to
 //             match (slot 8b + e of 32-key block u holds key
 //             32u + (e < 4 ? 4b + e : 16 + 4b + e - 4)).
-// K/V of tile j+1 are loaded into registers while tile j is computed, and
-// written to the second LDS buffer afterwards: one barrier per tile.
+// K/V of tile j+2 are loaded into registers while tile j is computed; tile
+// j+1 (loaded during tile j-1) is written to the second LDS buffer after
+// tile j's products: one barrier per tile.
 #include "prefill_tile.h"
 
 namespace cia {
@@ -82,23 +83,21 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
     // tail tile (the last one)
     const int nf = min(ntile, nfp8);
     const int qpos0 = a.past + q0 + n;
-    PfStage8 s8;
+    PfStage8 sa, sb;
     float c_cur = 1.0f, c_next = 1.0f;  // K scale of the tile being computed / staged
     if (nf > 0) {
-      pf_load8(a, g, 0, tid, s8);
-      c_cur = pf_scale(s8.ks);
-      pf_store8(lds[0], tid, s8, sel01, sel10);
-      if (nf > 1) pf_load8(a, g, 1, tid, s8);
+      pf_load8(a, g, 0, tid, sa);
+      c_cur = pf_scale(sa.ks);
+      pf_store8(lds[0], tid, sa, sel01, sel10);
+      if (nf > 1) pf_load8(a, g, 1, tid, sb);
     }
     __syncthreads();
-    for (int j = 0; j < nf; j++) {
-      // stage tile j+1 (loaded during tile j-1) into the free buffer, then
-      // start loading tile j+2
-      if (j + 1 < nf) {
-        c_next = pf_scale(s8.ks);
-        pf_store8(lds[(j + 1) & 1], tid, s8, sel01, sel10);
-        if (j + 2 < nf) pf_load8(a, g, j + 2, tid, s8);
-      }
+    // tile j: start loading tile j+2 (into ld), compute tile j, then stage
+    // tile j+1 (loaded during tile j-1, in st) into the free buffer, so a
+    // wave that finishes its products early stages while the other wave of
+    // its SIMD still computes
+    auto step = [&](int j, PfStage8& ld, PfStage8& st) {
+      if (j + 2 < nf) pf_load8(a, g, j + 2, tid, ld);
       // tiles past the wave's last query are skipped (wave-uniform).  The
       // score multiplier is kept >= 1e-30 so that masked keys (-inf) stay
       // -inf when a group's K scale is 0 (its scores are then ~0, as they
@@ -112,8 +111,17 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
           pf_tile<false>(lds[j & 1], lds[j & 1] + kPfTileBytes, qop, c, j == 0, 64 * j, qpos0,
                          n, b, O, mrun, lrun);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 1 < nf) {
+        c_next = pf_scale(st.ks);
+        pf_store8(lds[(j + 1) & 1], tid, st, sel01, sel10);
+      }
       c_cur = c_next;
       __syncthreads();
+    };
+    for (int j = 0; j < nf; j += 2) {
+      step(j, sa, sb);
+      if (j + 1 < nf) step(j + 1, sb, sa);
     }
     if (ntile > nf) {
       PfStage16 s16;
