@@ -457,6 +457,9 @@ def main():
 
     # ---- weights.bin upload: pinned double-buffered against one pageable buffer
     upload = upload_leg(a.upload_mib, dev, log) if a.upload_mib > 0 else None
+    # ---- tokenizer (host): encode throughput, the reference's beside it in
+    # the cpu_baseline leg
+    tokenizer = tokenizer_leg(log, with_reference=not a.no_cpu)
 
     # ---- CPU baseline: the oracle on this host's cores, one layer at a time
     cpu = None
@@ -517,6 +520,7 @@ def main():
         "long_context": long_ctx,
         "h2o": h2o,
         "weights_upload": upload,
+        "tokenizer": tokenizer,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
@@ -842,6 +846,51 @@ def cpu_prefill_baseline(S, seconds, log):
             "sample": f"oracle append of {S} tokens (whole) + attention_fused on the last "
                       f"{len(rows)} query rows, scaled by (query, key) pairs to all {S} rows; "
                       f"host {_host_model()}"}
+
+
+def tokenizer_leg(log, with_reference, mib=2):
+    """Host-side encode throughput of cia_tok_encode on ~2 MiB of synthetic
+    text with the synthetic byte-level BPE of tests/golden/tok; where
+    oracle/_ref/libreftok.so was built (the reference's tokenizer.h), the
+    same text through it beside (cpu_baseline leg only)."""
+    import random
+    from cuda_inf_amd.model_files import Tokenizer
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden", "tok")
+    rng = random.Random(3)
+    words = ["the", "capital", "of", "France", "is", "Paris", "über", "straße", "中文",
+             "don't", "they're", "12345", "3.14", "kato", "rien", "stion", "quai", "(x)", "--"]
+    parts, n = [], 0
+    while n < mib << 20:
+        w = rng.choice(words) + rng.choice([" ", " ", " ", "\n", ", "])
+        parts.append(w)
+        n += len(w.encode())
+    text = "".join(parts).encode()
+    t = Tokenizer()
+    if not t.load(d):
+        return None
+
+    def rate(fn):
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ids = fn(text)
+            el = time.perf_counter() - t0
+            best = el if best is None or el < best else best
+        return ids, len(text) / best / 1e6
+    ids, ours = rate(t.encode)
+    res = {"mb": round(len(text) / 1e6, 2), "tokens": len(ids), "mb_per_s": round(ours, 2),
+           "threads": 1}
+    if with_reference:
+        from oracle import model_files as om
+        if om.RefTokenizer.available():
+            ref = om.RefTokenizer(d)
+            rids, theirs = rate(ref.encode)
+            res["reference_mb_per_s"] = round(theirs, 2)
+            res["same_ids"] = rids == ids
+    log(f"tokenizer encode: {ours:.1f} MB/s on {len(text) / 1e6:.1f} MB ({len(ids)} tokens)"
+        + (f"; the reference's tokenizer.h {res['reference_mb_per_s']:.1f} MB/s, same ids: "
+           f"{res['same_ids']}" if "reference_mb_per_s" in res else ""))
+    return res
 
 
 def cpu_h2o_baseline(seconds, log, C=2048, W=256, P=1024):

@@ -20,6 +20,7 @@
 #include <cerrno>
 #include <climits>
 #include <memory>
+#include <mutex>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -266,6 +267,12 @@ struct cia_tokenizer {
     }
   }
 
+  // merged pieces already seen (pieces repeat: words), up to kCacheMax
+  // entries; encode calls on one tokenizer from several threads share it
+  static constexpr size_t kCacheMax = 1 << 16;
+  mutable std::mutex cache_mu;
+  mutable std::unordered_map<std::string, std::vector<int32_t>> cache;
+
   // one pre-tokenized piece (byte-level string) -> ids
   void bpe(const std::string& w, std::vector<int32_t>& out) const {
     auto it = sym.find(w);
@@ -273,6 +280,15 @@ struct cia_tokenizer {
       out.push_back(vid[it->second]);  // the whole piece is a token: no merges
       return;
     }
+    {
+      std::lock_guard<std::mutex> g(cache_mu);
+      auto c = cache.find(w);
+      if (c != cache.end()) {
+        out.insert(out.end(), c->second.begin(), c->second.end());
+        return;
+      }
+    }
+    const size_t first = out.size();
     std::vector<int32_t> s;
     for (size_t i = 0; i < w.size();) {
       const int k = lead_len((unsigned char)w[i]);
@@ -297,6 +313,9 @@ struct cia_tokenizer {
     }
     for (int32_t x : s)
       if (vid[x] != INT32_MIN) out.push_back(vid[x]);
+    std::lock_guard<std::mutex> g(cache_mu);
+    if (cache.size() < kCacheMax)
+      cache.emplace(w, std::vector<int32_t>(out.begin() + (ptrdiff_t)first, out.end()));
   }
 
   void encode_chunk(const char* t, size_t n, std::vector<int32_t>& out) const {
