@@ -267,8 +267,11 @@ struct cia_tokenizer {
     }
   }
 
-  // merged pieces already seen (pieces repeat: words), up to kCacheMax
-  // entries; encode calls on one tokenizer from several threads share it
+  // raw bytes of every token whose byte-level string is made of table
+  // characters -> its id (a piece is a whole token iff its raw bytes are
+  // here); merged pieces already seen, by raw bytes (pieces repeat: words),
+  // up to kCacheMax entries, shared by encode calls from several threads
+  std::unordered_map<std::string, int32_t> raw_vocab;
   static constexpr size_t kCacheMax = 1 << 16;
   mutable std::mutex cache_mu;
   mutable std::unordered_map<std::string, std::vector<int32_t>> cache;
@@ -280,15 +283,6 @@ struct cia_tokenizer {
       out.push_back(vid[it->second]);  // the whole piece is a token: no merges
       return;
     }
-    {
-      std::lock_guard<std::mutex> g(cache_mu);
-      auto c = cache.find(w);
-      if (c != cache.end()) {
-        out.insert(out.end(), c->second.begin(), c->second.end());
-        return;
-      }
-    }
-    const size_t first = out.size();
     std::vector<int32_t> s;
     for (size_t i = 0; i < w.size();) {
       const int k = lead_len((unsigned char)w[i]);
@@ -313,9 +307,6 @@ struct cia_tokenizer {
     }
     for (int32_t x : s)
       if (vid[x] != INT32_MIN) out.push_back(vid[x]);
-    std::lock_guard<std::mutex> g(cache_mu);
-    if (cache.size() < kCacheMax)
-      cache.emplace(w, std::vector<int32_t>(out.begin() + (ptrdiff_t)first, out.end()));
   }
 
   void encode_chunk(const char* t, size_t n, std::vector<int32_t>& out) const {
@@ -323,15 +314,41 @@ struct cia_tokenizer {
     std::vector<int> ends;
     code_points(t, n, cps);
     pieces(cps, ends);
+    // the chunk re-encoded from its code points (the text itself when it is
+    // valid UTF-8) and each code point's offset in it
+    std::string renc;
+    std::vector<uint32_t> off(cps.size() + 1);
+    for (size_t i = 0; i < cps.size(); i++) {
+      off[i] = (uint32_t)renc.size();
+      put_utf8(cps[i], renc);
+    }
+    off[cps.size()] = (uint32_t)renc.size();
     std::string raw, bl;
     int a = 0;
     for (int e : ends) {
-      raw.clear();
-      for (int i = a; i < e; i++) put_utf8(cps[i], raw);
+      raw.assign(renc, off[a], off[e] - off[a]);
+      a = e;
+      // a whole-piece token, or a piece merged before: no byte-level string
+      auto v = raw_vocab.find(raw);
+      if (v != raw_vocab.end()) {
+        out.push_back(v->second);
+        continue;
+      }
+      {
+        std::lock_guard<std::mutex> g(cache_mu);
+        auto c = cache.find(raw);
+        if (c != cache.end()) {
+          out.insert(out.end(), c->second.begin(), c->second.end());
+          continue;
+        }
+      }
       bl.clear();
       for (unsigned char b : raw) bl += byte_char[b];
+      const size_t first = out.size();
       bpe(bl, out);
-      a = e;
+      std::lock_guard<std::mutex> g(cache_mu);
+      if (cache.size() < kCacheMax)
+        cache.emplace(raw, std::vector<int32_t>(out.begin() + (ptrdiff_t)first, out.end()));
     }
   }
 
@@ -546,6 +563,19 @@ extern "C" int cia_tok_load(const char* dir, cia_tokenizer** out) {
     std::stable_sort(sp.begin(), sp.end(),
                      [](const auto& x, const auto& y) { return x.first.size() > y.first.size(); });
     for (auto& x : sp) t->special_by_byte[(unsigned char)x.first[0]].push_back(x);
+    for (const auto& e : t->sym) {
+      if (t->vid[(size_t)e.second] == INT32_MIN) continue;
+      std::string raw;
+      bool ok = true;
+      for (size_t i = 0; i < e.first.size() && ok;) {
+        const int k = lead_len((unsigned char)e.first[i]);
+        auto c = t->char_byte.find(e.first.substr(i, (size_t)k));
+        ok = c != t->char_byte.end() && i + (size_t)k <= e.first.size();
+        if (ok) raw.push_back((char)c->second);
+        i += (size_t)k;
+      }
+      if (ok) t->raw_vocab[raw] = t->vid[(size_t)e.second];
+    }
     *out = t.release();
     return CIA_OK;
   });
