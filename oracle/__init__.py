@@ -1,6 +1,6 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so).
 
-TEST INFRASTRUCTURE ONLY: the oracle is the checker.  Only tests/,
+TEST INFRASTRUCTURE ONLY: the HIP path is compared against it.  Only tests/,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` import
 this module.  The product package ``cuda_inf_amd`` never does.
 

@@ -1,7 +1,7 @@
 """CPU restatement of the reference's model-file handling: the weight index
 reader and the byte-level BPE tokenizer, in plain Python.
 
-TEST INFRASTRUCTURE ONLY: the oracle is the checker.  Only tests/ import
+TEST INFRASTRUCTURE ONLY: the product is compared against it.  Only tests/ import
 this module; the product (cuda_inf_amd, include/cuda_inf_model.h) never does.
 
 Pinned by tests/test_oracle_model_files.py:

@@ -1,8 +1,8 @@
 /*
  * oracle.c -- scalar CPU restatement of the cuda_inf attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or
- * shipped).  Loaded by tests/, __graft_entry__.smoke() and bench.py's
+ * TEST INFRASTRUCTURE ONLY (what the HIP path is compared against, never
+ * the thing measured or shipped).  Loaded by tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg, nowhere else.
  *
  * Reference: g023/cuda_inf src/engine.cu (cited as engine.cu:LINE).  The

@@ -1,8 +1,8 @@
 /*
  * oracle.h -- scalar CPU restatement of the cuda_inf attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path is
- * compared against.  Only tests/, __graft_entry__.smoke() and the cpu_baseline
+ * TEST INFRASTRUCTURE ONLY.  This library is what the HIP path is compared
+ * against.  Only tests/, __graft_entry__.smoke() and the cpu_baseline
  * leg of bench.py may load it.  Nothing in cuda_inf_amd/ links or calls it.
  *
  * Every function restates one piece of the reference engine (src/engine.cu of

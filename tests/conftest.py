@@ -9,7 +9,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-# north_star tolerance for attention outputs against the fp32 oracle
+# the attention path's tolerance for outputs against the fp32 oracle
 ATOL = 2e-3
 RTOL = 1e-3
 

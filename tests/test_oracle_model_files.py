@@ -1,5 +1,5 @@
-"""Pins the oracle of the model files (oracle/model_files.py) before it is
-used as the checker:
+"""Pins the oracle of the model files (oracle/model_files.py) before the
+product is compared against it:
   - the index reader against an index assembled by hand, field by field
     (tools/make_index.py:3-11);
   - the pre-tokenizer against the `regex` module evaluating the split
