@@ -31,7 +31,8 @@
 //             32u + (e < 4 ? 4b + e : 16 + 4b + e - 4)).
 // K/V of tile j+2 are loaded into registers while tile j is computed; tile
 // j+1 (loaded during tile j-1) is written to the second LDS buffer after
-// tile j's products: one barrier per tile.
+// tile j's products, by waves 0-3 alone (of the two waves of a SIMD, the
+// older one's products finish first): one barrier per tile.
 #include "prefill_tile.h"
 
 namespace cia {
@@ -83,21 +84,42 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
     // tail tile (the last one)
     const int nf = min(ntile, nfp8);
     const int qpos0 = a.past + q0 + n;
-    PfStage8 sa, sb;
+    // waves 0-3 (the older wave of each SIMD, whose products finish first)
+    // stage whole tiles: thread tid its own half and that of tid + 256;
+    // waves 4-7 fetch only the group's K scale
+    struct Stage2 {
+      PfStage8 lo, hi;
+    };
+    const bool stager = w < 4;
+    auto load2 = [&](int j, Stage2& st) {
+      if (stager) {
+        pf_load8(a, g, j, tid, st.lo);
+        pf_load8(a, g, j, tid + 256, st.hi);
+      } else {
+        st.lo.ks = a.ksc[j * NKV + g];
+      }
+    };
+    auto store2 = [&](uint8_t* buf, const Stage2& st) {
+      if (stager) {
+        pf_store8(buf, tid, st.lo, sel01, sel10);
+        pf_store8(buf, tid + 256, st.hi, sel01, sel10);
+      }
+    };
+    Stage2 sa, sb;
     float c_cur = 1.0f, c_next = 1.0f;  // K scale of the tile being computed / staged
     if (nf > 0) {
-      pf_load8(a, g, 0, tid, sa);
-      c_cur = pf_scale(sa.ks);
-      pf_store8(lds[0], tid, sa, sel01, sel10);
-      if (nf > 1) pf_load8(a, g, 1, tid, sb);
+      load2(0, sa);
+      c_cur = pf_scale(sa.lo.ks);
+      store2(lds[0], sa);
+      if (nf > 1) load2(1, sb);
     }
     __syncthreads();
     // tile j: start loading tile j+2 (into ld), compute tile j, then stage
     // tile j+1 (loaded during tile j-1, in st) into the free buffer, so a
     // wave that finishes its products early stages while the other wave of
     // its SIMD still computes
-    auto step = [&](int j, PfStage8& ld, PfStage8& st) {
-      if (j + 2 < nf) pf_load8(a, g, j + 2, tid, ld);
+    auto step = [&](int j, Stage2& ld, Stage2& st) {
+      if (j + 2 < nf) load2(j + 2, ld);
       // tiles past the wave's last query are skipped (wave-uniform).  The
       // score multiplier is kept >= 1e-30 so that masked keys (-inf) stay
       // -inf when a group's K scale is 0 (its scores are then ~0, as they
@@ -113,8 +135,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void k_prefill_mfma(PrefillArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < nf) {
-        c_next = pf_scale(st.ks);
-        pf_store8(lds[(j + 1) & 1], tid, st, sel01, sel10);
+        c_next = pf_scale(st.lo.ks);
+        store2(lds[(j + 1) & 1], st);
       }
       c_cur = c_next;
       __syncthreads();
