@@ -122,7 +122,19 @@ __host__ __device__ inline AppendShape append_shape(int slot0, int S) {
   return a;
 }
 
-// grid = (1 + nfull, 8 kv heads), block = 256
+// The source token of tail row r after the append (the reference leaves
+// row r holding the token the last op that wrote row r put there), or -1
+// when the append does not write row r.
+__device__ __forceinline__ int append_tail_src(int r, const AppendShape& sh) {
+  if (!sh.commit0) return r >= sh.slot0 && r < sh.slot0 + sh.S ? r - sh.slot0 : -1;
+  if (r < sh.cnt_last) return sh.s_last + r;
+  if (sh.nfull > 0) return sh.cnt0 + G * (sh.nfull - 1) + r;
+  return r >= sh.slot0 ? r - sh.slot0 : -1;
+}
+
+// grid = (1 + nfull, 8 kv heads), block = 256.  Workgroup (0, h) also
+// writes kv head h's tail rows, after its own reads of the old ones (the
+// only reads of the tail in the launch), so no second launch is needed.
 __global__ __launch_bounds__(256) void k_append_commit(const uint16_t* __restrict__ ktail,
                                                        const uint16_t* __restrict__ vtail,
                                                        const uint16_t* __restrict__ k,
@@ -137,6 +149,20 @@ __global__ __launch_bounds__(256) void k_append_commit(const uint16_t* __restric
   const int src0 = g == 0 ? 0 : sh.cnt0 + G * (g - 1);
   commit_group_rows(ktail, vtail, k, v, slot, src0, kc8, vc8, ksc, vsc, committed + G * g,
                     committed / G + g, blockIdx.y, threadIdx.x);
+  // (every thread's tail reads finished before the barrier inside)
+  if (g == 0) {
+    const int r = threadIdx.x >> 2, c = (threadIdx.x & 3) * 16, h = blockIdx.y;
+    const int src = append_tail_src(r, sh);
+    if (src >= 0) {
+      const size_t o = ((size_t)r * NKV + h) * D + c, i = ((size_t)src * NKV + h) * D + c;
+      const u32x4 k0 = *(const u32x4*)(k + i), k1 = *(const u32x4*)(k + i + 8);
+      const u32x4 v0 = *(const u32x4*)(v + i), v1 = *(const u32x4*)(v + i + 8);
+      *(u32x4*)(ktail + o) = k0;
+      *(u32x4*)(ktail + o + 8) = k1;
+      *(u32x4*)(vtail + o) = v0;
+      *(u32x4*)(vtail + o + 8) = v1;
+    }
+  }
 }
 
 // The tail as the reference leaves it: row r holds the token the last op
@@ -148,16 +174,7 @@ __global__ __launch_bounds__(64) void k_append_tail(uint16_t* __restrict__ ktail
                                                     const uint16_t* __restrict__ v,
                                                     AppendShape sh) {
   const int r = blockIdx.x;
-  int src = -1;
-  if (!sh.commit0) {
-    if (r >= sh.slot0 && r < sh.slot0 + sh.S) src = r - sh.slot0;
-  } else if (r < sh.cnt_last) {
-    src = sh.s_last + r;
-  } else if (sh.nfull > 0) {
-    src = sh.cnt0 + G * (sh.nfull - 1) + r;
-  } else if (r >= sh.slot0) {
-    src = r - sh.slot0;
-  }
+  const int src = append_tail_src(r, sh);
   if (src < 0) return;
   const size_t o = (size_t)threadIdx.x * 8;  // element offset inside the row (8 heads x 64)
   *(u32x4*)(ktail + (size_t)r * NKV * D + o) = *(const u32x4*)(k + (size_t)src * NKV * D + o);
@@ -385,13 +402,12 @@ extern "C" __attribute__((visibility("hidden"))) int cia_kv_append_batched(
   const AppendShape sh = append_shape(past - c, S);
   const int ncommit = sh.commit0 ? 1 + sh.nfull : 0;
   hipStream_t s = (hipStream_t)stream;
-  if (ncommit) {
+  // (with a commit, its first workgroup per kv head also writes the tail)
+  if (ncommit)
     hipLaunchKernelGGL(k_append_commit, dim3(ncommit, NKV), dim3(256), 0, s, ktail, vtail, k, v,
                        kc8, vc8, ksc, vsc, sh, c);
-    const int st = launch_status();
-    if (st) return st;
-  }
-  hipLaunchKernelGGL(k_append_tail, dim3(G), dim3(64), 0, s, ktail, vtail, k, v, sh);
+  else
+    hipLaunchKernelGGL(k_append_tail, dim3(G), dim3(64), 0, s, ktail, vtail, k, v, sh);
   const int st = launch_status();
   if (st) return st;
   *committed = c + G * ncommit;
