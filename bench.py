@@ -66,8 +66,14 @@ def main():
                          "projections, producers, attention, out_proj + residual (0 = skip)")
     ap.add_argument("--h2o-steps", type=int, default=4000,
                     help="H2O decode steps after a 1024-token prompt (0 = skip)")
-    ap.add_argument("--upload-mib", type=int, default=1024,
+    ap.add_argument("--upload-mib", type=int, default=0,
                     help="weights.bin upload leg: MiB of synthetic file (0 = skip)")
+    ap.add_argument("--tokenizer", action="store_true",
+                    help="host tokenizer leg (encode throughput; the reference's tokenizer.h "
+                         "timed beside it under cpu_baseline)")
+    ap.add_argument("--split-steps", type=int, default=32,
+                    help="decode tokens through the reference's split + combine (16 splits) "
+                         "at the headline context (0 = skip)")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="MiB: first run a plain device copy of this size three times "
                          "(the reference dispatch that scales rocprofv3 byte counters)")
@@ -85,7 +91,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
-    total_steps = W + 2 * K + a.cold_steps + a.prep_steps + a.block_steps
+    total_steps = W + 2 * K + a.cold_steps + a.prep_steps + a.block_steps + a.split_steps
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
@@ -240,6 +246,51 @@ def main():
         log(f"cold: median {cold_us:.2f} us/token; plain read cold {floor_cold_us:.2f} us/token")
     mean_tok_bytes = timed_bytes / K
 
+    # ---- the reference's launch shape at the same context: per layer the
+    # append launch, attn_decode_split with 16 splits and attn_decode_combine
+    # (engine.cu:830-852), split and combine event-bracketed separately
+    split16 = None
+    if a.split_steps > 4:
+        ns = 16
+        sbufs = []
+        for l in range(nL):
+            pm = torch.zeros(NH * ns, dtype=torch.float32, device=dev)
+            pl = torch.zeros(NH * ns, dtype=torch.float32, device=dev)
+            po = torch.zeros(NH * ns * D, dtype=torch.float32, device=dev)
+            sbufs.append((pm, pl, po))
+            arr[l].nsplit, arr[l].pm, arr[l].pl, arr[l].po = ns, pm.data_ptr(), pl.data_ptr(), po.data_ptr()
+        n_ev = 2
+        n = a.split_steps - 2 - n_ev
+        run(2)
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        run(n)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        sp_us = c0.elapsed_time(c1) * 1e3 / n
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(3 * n_ev * nL)]
+        for e in evs:  # the hipEvent_t handles exist once recorded
+            e.record(stream)
+        torch.cuda.synchronize()
+        run(n_ev, (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs]))
+        torch.cuda.synchronize()
+        first = sorted(evs[3 * r].elapsed_time(evs[3 * r + 1]) * 1e3 for r in range(n_ev * nL))
+        second = sorted(evs[3 * r + 1].elapsed_time(evs[3 * r + 2]) * 1e3 for r in range(n_ev * nL))
+        for l in range(nL):
+            arr[l].nsplit = 0
+        del sbufs
+        s_bytes = bytes_of_steps(cur["step"] - n_ev - n, n) / n
+        split16 = {"us_per_token": round(sp_us, 2), "tokens": n,
+                   "gbps": round(s_bytes / (sp_us * 1e-6) / 1e9, 1),
+                   "split_us_median": round(first[len(first) // 2], 2),
+                   "combine_us_median": round(second[len(second) // 2], 2),
+                   "launches": "append (k_append_tail / k_append_commit), k_decode split mode, "
+                               "k_decode_combine_small per layer"}
+        log(f"split+combine (16 splits) at {ctx}: {sp_us:.2f} us/token; split "
+            f"{split16['split_us_median']} us + combine {split16['combine_us_median']} us per "
+            f"layer (event-bracketed medians)")
+
     # ---- QK producers fused: the same layers take raw q / k, and the decode
     # kernels run per-head RMSNorm + RoPE (engine.cu:799-801) themselves
     prep = None
@@ -337,7 +388,7 @@ def main():
                  "event_bracketed_us": {"qkv_proj": round(med[0], 2), "attention": round(med[1], 2),
                                         "out_proj_residual": round(med[2], 2)},
                  "int4_weight_bytes_per_layer": wbytes,
-                 "launches_per_layer": 4,
+                 "launches_per_layer": 3,
                  "kernels": "k_gemv_int4 (q/k/v), k_decode (producers inside), "
                             "k_gemv_int4 (out_proj + residual)"}
         log(f"attention branch (INT4 projections + attention): {blk_us:.2f} us/token; "
@@ -457,9 +508,10 @@ def main():
 
     # ---- weights.bin upload: pinned double-buffered against one pageable buffer
     upload = upload_leg(a.upload_mib, dev, log) if a.upload_mib > 0 else None
-    # ---- tokenizer (host): encode throughput, the reference's beside it in
-    # the cpu_baseline leg
-    tokenizer = tokenizer_leg(log, with_reference=not a.no_cpu)
+    # ---- tokenizer (host): encode throughput; the reference's tokenizer.h
+    # on the same text goes to the cpu_baseline block
+    tokenizer, tok_ref = (tokenizer_leg(log, with_reference=not a.no_cpu) if a.tokenizer
+                          else (None, None))
 
     # ---- CPU baseline: the oracle on this host's cores, one layer at a time
     cpu = None
@@ -473,6 +525,8 @@ def main():
             cpu_prefill = cpu_prefill_baseline(a.prefill, a.cpu_seconds, log)
         if a.h2o_steps > 0:
             cpu_h2o = cpu_h2o_baseline(a.cpu_seconds, log)
+    if cpu is not None and tok_ref is not None:
+        cpu["tokenizer_reference"] = tok_ref
     if prefill is not None:
         prefill["cpu_baseline"] = cpu_prefill
     if h2o is not None:
@@ -515,6 +569,7 @@ def main():
                          "cold_us_per_token": round(floor_cold_us, 3) if floor_cold_us else None,
                          "cold_frac": round(floor_cold_us / cold_us, 4) if floor_cold_us else None}},
         "prefill": prefill,
+        "split16": split16,
         "qk_producers_fused": prep,
         "attention_branch": block,
         "long_context": long_ctx,
@@ -850,9 +905,10 @@ def cpu_prefill_baseline(S, seconds, log):
 
 def tokenizer_leg(log, with_reference, mib=2):
     """Host-side encode throughput of cia_tok_encode on ~2 MiB of synthetic
-    text with the synthetic byte-level BPE of tests/golden/tok; where
-    oracle/_ref/libreftok.so was built (the reference's tokenizer.h), the
-    same text through it beside (cpu_baseline leg only)."""
+    text with the synthetic byte-level BPE of tests/golden/tok.  Returns
+    (ours, reference): where oracle/_ref/libreftok.so was built (the
+    reference's tokenizer.h), the same text through it, for the
+    cpu_baseline block."""
     import random
     from cuda_inf_amd.model_files import Tokenizer
     d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden", "tok")
@@ -867,7 +923,7 @@ def tokenizer_leg(log, with_reference, mib=2):
     text = "".join(parts).encode()
     t = Tokenizer()
     if not t.load(d):
-        return None
+        return None, None
 
     def rate(fn):
         best = None
@@ -880,17 +936,20 @@ def tokenizer_leg(log, with_reference, mib=2):
     ids, ours = rate(t.encode)
     res = {"mb": round(len(text) / 1e6, 2), "tokens": len(ids), "mb_per_s": round(ours, 2),
            "threads": 1}
+    ref_res = None
     if with_reference:
         from oracle import model_files as om
         if om.RefTokenizer.available():
             ref = om.RefTokenizer(d)
             rids, theirs = rate(ref.encode)
-            res["reference_mb_per_s"] = round(theirs, 2)
-            res["same_ids"] = rids == ids
+            ref_res = {"value": round(theirs, 2), "unit": "MB/s", "cores": 1,
+                       "kind": "reference", "same_ids": rids == ids,
+                       "sample": f"{len(text) / 1e6:.1f} MB of synthetic text, synthetic "
+                                 f"byte-level BPE vocabulary (tests/golden/tok)"}
     log(f"tokenizer encode: {ours:.1f} MB/s on {len(text) / 1e6:.1f} MB ({len(ids)} tokens)"
-        + (f"; the reference's tokenizer.h {res['reference_mb_per_s']:.1f} MB/s, same ids: "
-           f"{res['same_ids']}" if "reference_mb_per_s" in res else ""))
-    return res
+        + (f"; the reference's tokenizer.h {ref_res['value']:.1f} MB/s, same ids: "
+           f"{ref_res['same_ids']}" if ref_res else ""))
+    return res, ref_res
 
 
 def cpu_h2o_baseline(seconds, log, C=2048, W=256, P=1024):

@@ -38,6 +38,9 @@ SIGNATURES = {
     "cia_attention_fused": (_I, [_P] * 7 + [_I, _P, _P, _I, _I, _F, _P, ctypes.c_int64, _P]),
     "cia_attention_fused_fp8": (_I, [_P] * 7 + [_I, _P, _I, _I, _F, _P]),
     "cia_attn_decode_split": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I, _P]),
+    "cia_attn_decode_split_ws": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I, _P,
+                                                ctypes.c_int64, _P]),
+    "cia_split_workspace_bytes": (ctypes.c_int64, [_I]),
     "cia_attn_decode_combine": (_I, [_P, _P, _P, _P, _I, _P]),
     "cia_attn_decode": (_I, [_P] * 7 + [_I, _I, _F, _P, _P, ctypes.c_int64, _P]),
     "cia_decode_workspace_bytes": (ctypes.c_int64, [_I]),

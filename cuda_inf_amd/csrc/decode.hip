@@ -163,7 +163,8 @@ constexpr int kSplitMfmaMinKeys = 128;
 extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed, int qpos,
-    float scale, float* pm, float* pl, float* po, int nsplit, void* stream);
+    float scale, float* pm, float* pl, float* po, int nsplit, void* ws, void* stream);
+extern "C" int64_t cia_split_workspace_bytes(int nsplit);
 
 static int check_cache(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
                        const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
@@ -176,11 +177,12 @@ static int check_cache(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8
   return CIA_OK;
 }
 
-extern "C" int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
-                                     const uint16_t* ksc, const uint16_t* vsc,
-                                     const uint16_t* ktail, const uint16_t* vtail, int committed,
-                                     int qpos, float scale, float* pm, float* pl, float* po,
-                                     int nsplit, void* stream) {
+// cia_attn_decode_split with ws (the caller's workspace, or NULL for the
+// library's device array)
+static int decode_split(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                        const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
+                        const uint16_t* vtail, int committed, int qpos, float scale, float* pm,
+                        float* pl, float* po, int nsplit, void* ws, void* stream) {
   int st = check_cache(q, kc8, vc8, ksc, vsc, ktail, vtail, committed);
   if (st) return st;
   CIA_REQUIRE(pm && pl && po, CIA_ERR_NULL);
@@ -188,11 +190,33 @@ extern "C" int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8, cons
   CIA_REQUIRE(qpos - committed < G, CIA_ERR_STATE);  // the tail holds at most 64 keys
   if (nsplit <= kSplitMfmaMax && (qpos + nsplit) / nsplit >= kSplitMfmaMinKeys)
     return cia_split_mfma(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, qpos, scale, pm, pl, po,
-                          nsplit, stream);
+                          nsplit, ws, stream);
   Group64Cache c{kc8, vc8, ksc, vsc, ktail, vtail, committed};
   hipLaunchKernelGGL(k_decode_split, dim3(NKV, nsplit), dim3(256), 0, (hipStream_t)stream, q, c,
                      qpos, scale, pm, pl, po, nsplit);
   return launch_status();
+}
+
+extern "C" int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                                     const uint16_t* ksc, const uint16_t* vsc,
+                                     const uint16_t* ktail, const uint16_t* vtail, int committed,
+                                     int qpos, float scale, float* pm, float* pl, float* po,
+                                     int nsplit, void* stream) {
+  return decode_split(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, qpos, scale, pm, pl, po,
+                      nsplit, nullptr, stream);
+}
+
+extern "C" int cia_attn_decode_split_ws(const uint16_t* q, const uint8_t* kc8,
+                                        const uint8_t* vc8, const uint16_t* ksc,
+                                        const uint16_t* vsc, const uint16_t* ktail,
+                                        const uint16_t* vtail, int committed, int qpos,
+                                        float scale, float* pm, float* pl, float* po, int nsplit,
+                                        void* ws, int64_t ws_bytes, void* stream) {
+  CIA_REQUIRE(ws, CIA_ERR_NULL);
+  CIA_REQUIRE(nsplit >= 1 && ws_bytes >= cia_split_workspace_bytes(nsplit), CIA_ERR_ARG);
+  CIA_REQUIRE(aligned(ws, 16), CIA_ERR_ALIGN);
+  return decode_split(q, kc8, vc8, ksc, vsc, ktail, vtail, committed, qpos, scale, pm, pl, po,
+                      nsplit, ws, stream);
 }
 
 extern "C" int cia_attn_decode_combine(const float* pm, const float* pl, const float* po,

@@ -64,7 +64,6 @@
 //   - a device-scope atomic round trip: about 0.25 us idle, 0.4-0.5 us under
 //     the stream; the acknowledgement of agent-coherent stores about 0.6 us.
 #include <algorithm>
-#include <map>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -106,6 +105,14 @@ constexpr int64_t kPartBytes = (int64_t)NKV * kMaxRanges * kPartF * sizeof(float
 constexpr int64_t kWsBytes = kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
 // the split entry's workspace: two share slots per (kv head, range), then the counters
 constexpr int64_t kSplitWsBytes = 2 * kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
+
+// The drop-in split entry's shares meet in this file-scope device array
+// (two share slots per (kv head, range), then the arrival counters) unless
+// the caller passes a workspace: cia_attn_decode_split allocates nothing.
+// The kernels address it from device code.  The counters are zero at load,
+// cleared again by a fill kernel on the first call on a device, and every
+// complete call leaves them at zero; calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t split_scratch[kSplitWsBytes];
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
@@ -150,6 +157,21 @@ __device__ __forceinline__ u32x2 ds_read_tr8_at(const uint8_t* p) {
 // use is scheduled before it
 __device__ __forceinline__ void lds_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
+// Publishing a partial to the other workgroups: its agent-coherent stores
+// (relaxed agent-scope atomics) are acknowledged -- vmcnt(0): a store's
+// count drops when the L2 of this XCD has written it through -- before the
+// caller's barrier and its relaxed ticket increment, which another
+// workgroup's coherent loads then follow.  The wait builtin has no memory
+// semantics for the compiler, so compiler-only fences (no instruction) keep
+// the stores above it and the ticket below it.
+__device__ __forceinline__ void stores_acked() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  asm volatile("" ::: "memory");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
@@ -958,6 +980,9 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
   // ================================================================ merge
   if (w >= kFpWaves) return;  // (tail waves: their partial is in LDS)
   if constexpr (kSplit) {
+    // the shares' workspace: the caller's, else the library's device array
+    float* const part = a.part ? a.part : (float*)split_scratch;
+    uint32_t* const cnt = a.part ? a.cnt : (uint32_t*)(split_scratch + 2 * kPartBytes);
     // the tail waves' partial of split sp (head i, dim d) folded into a
     // split's (M, L, O) in log2 units
     auto fold_tail = [&](int sp, int i, int d, float& M, float& L, float& O) {
@@ -1031,7 +1056,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
           if (sp >= tlo && sp <= thi) fold_tail(sp, i, d, M, L, O);
           write_split(sp, M, L, O);
         } else {
-          float* row = a.part + ((size_t)(g * 2 * kMaxRanges + 2 * r + j) * GQA + i) * kPartRow;
+          float* row = part + ((size_t)(g * 2 * kMaxRanges + 2 * r + j) * GQA + i) * kPartRow;
           __hip_atomic_store(row + 4 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           if (d == 0) {
             __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1039,7 +1064,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
           }
         }
       }
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the shares have reached the agent
+      stores_acked();  // the shares have reached the agent
       __builtin_amdgcn_s_barrier();        // the workgroup's shares stored
       // a ticket per shared split: lane 0 of waves 0 and 1 (splits s0, s0 + 1)
       uint32_t* sticket = (uint32_t*)(lds + kLdsTicket);
@@ -1047,7 +1072,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         int rl, rh;
         writers(s0 + w, rl, rh);
         if (rl != rh)
-          sticket[w] = __hip_atomic_fetch_add(a.cnt + g * kCntStride + s0 + w, 1u, __ATOMIC_RELAXED,
+          sticket[w] = __hip_atomic_fetch_add(cnt + g * kCntStride + s0 + w, 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1060,8 +1085,8 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         // ---- the last share of split sp to arrive: every share stored.  The
         // counter goes back to zero for the next call.  Shares in range order.
         if (i == 0 && d == 0)
-          __hip_atomic_store(a.cnt + g * kCntStride + sp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.part + (size_t)g * 2 * kMaxRanges * GQA * kPartRow);
+          __hip_atomic_store(cnt + g * kCntStride + sp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(part + (size_t)g * 2 * kMaxRanges * GQA * kPartRow);
         float M = -1e30f, L = 0.f, O = 0.f;
         for (int p0 = rl; p0 <= rh; p0 += 8) {
           float mp[8], lp[8], op[8];
@@ -1130,13 +1155,13 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         if (a.sub <= 1 && sp >= tlo && sp <= thi) fold_tail(sp, i, d, M, L, Oacc);
         if (a.sub > 1) {
           // this workgroup's share of the split, for the last to arrive
-          float* row = a.part + ((size_t)(g * kMaxRanges + r) * GQA + i) * kPartRow;
+          float* row = part + ((size_t)(g * kMaxRanges + r) * GQA + i) * kPartRow;
           __hip_atomic_store(row + 4 + d, Oacc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           if (d == 0) {
             __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
-          __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have reached the agent
+          stores_acked();
           continue;
         }
         a.po[((size_t)h * a.nsplit + sp) * D + d] = Oacc;
@@ -1148,7 +1173,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     }
     if (a.sub <= 1) return;
     __builtin_amdgcn_s_barrier();  // the workgroup's share stored
-    uint32_t* ctr = a.cnt + g * kCntStride + s0;
+    uint32_t* ctr = cnt + g * kCntStride + s0;
     uint32_t* sticket = (uint32_t*)(lds + kLdsTicket);
     if (tid == 0) *sticket = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1160,7 +1185,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     if (tid < GQA * D) {
       const int i = tid >> 6, d = tid & 63, h = g * GQA + i;
       const __amdgpu_buffer_rsrc_t rs =
-          buf_rsrc(a.part + (size_t)(g * kMaxRanges + s0 * a.sub) * GQA * kPartRow);
+          buf_rsrc(part + (size_t)(g * kMaxRanges + s0 * a.sub) * GQA * kPartRow);
       // shares 8 at a time (the loads of a batch go out together)
       float M = -1e30f, L = 0.f, O = 0.f;
       for (int p0 = 0; p0 < a.sub; p0 += 8) {
@@ -1228,7 +1253,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
         __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores have reached the agent
+      stores_acked();
     }
   }
   if (R == 1) return;
@@ -1456,41 +1481,39 @@ int scratch_for_device(void** out, hipStream_t s) {
   return CIA_OK;
 }
 
-// The split entry's share workspace (kSplitWsBytes: two share slots per
-// (kv head, range), then the counters), one per (device, stream):
-// allocated and its counters cleared on the first call
-// on a stream, kept until the process ends.  Calls on one stream run in
-// order, and calls on different streams use different workspaces.
-std::mutex g_split_mu;
-std::map<std::pair<int, hipStream_t>, void*> g_split_ws;
+// split_scratch's counters cleared by a fill kernel (no memset node, so the
+// call stays capturable) on the first call on a device.  A first call made
+// under stream capture records the fill into the graph (each replay clears
+// the counters before its split launch, harmlessly) and leaves the device
+// unmarked, so the next eager call clears them too.
+__global__ void k_zero_split_counters() {
+  uint32_t* c = (uint32_t*)(split_scratch + 2 * kPartBytes);
+  for (int i = threadIdx.x; i < NKV * kCntStride; i += blockDim.x) c[i] = 0u;
+}
 
-int split_ws_for_stream(void** out, hipStream_t s) {
+std::mutex g_split_mu;
+bool g_split_ready[kMaxDevices];
+
+int split_scratch_prepare(hipStream_t s) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
     set_hip_error(e);
     return CIA_ERR_HIP;
   }
+  if (dev < 0 || dev >= kMaxDevices) return CIA_ERR_ARG;
   std::lock_guard<std::mutex> lock(g_split_mu);
-  const auto key = std::make_pair(dev, s);
-  auto it = g_split_ws.find(key);
-  if (it == g_split_ws.end()) {
-    void* p = nullptr;
-    e = hipMalloc(&p, kSplitWsBytes);
-    if (e != hipSuccess) {
-      set_hip_error(e);
-      return CIA_ERR_HIP;
-    }
-    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, s,
-                       (uint32_t*)((char*)p + 2 * kPartBytes), NKV * kCntStride);
-    const int st = launch_status();
-    if (st) {
-      (void)hipFree(p);
-      return st;
-    }
-    it = g_split_ws.emplace(key, p).first;
+  if (g_split_ready[dev]) return CIA_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(s, &cs);
+  if (e != hipSuccess) {
+    set_hip_error(e);
+    return CIA_ERR_HIP;
   }
-  *out = it->second;
+  hipLaunchKernelGGL(k_zero_split_counters, dim3(1), dim3(256), 0, s);
+  const int st = launch_status();
+  if (st) return st;
+  if (cs == hipStreamCaptureStatusNone) g_split_ready[dev] = true;
   return CIA_OK;
 }
 
@@ -1517,15 +1540,21 @@ extern "C" int cia_attn_decode_noalloc(const uint16_t* q, const uint8_t* kc8, co
                          nullptr);
 }
 
+extern "C" int64_t cia_split_workspace_bytes(int nsplit) {
+  return nsplit < 1 ? 0 : kSplitWsBytes;
+}
+
 // The reference's split partials on the matrix cores, one launch of
 // k_decode<false, true> (the tail keys folded in by the split's writer).
 // Fewer splits than ranges are each spread over several workgroups, which
-// meet in a workspace the library holds per stream.  Internal entry of
-// cia_attn_decode_split for nsplit <= kSplitMfmaMax (arguments checked there).
+// meet in ws (the caller's workspace of kSplitWsBytes, counters zeroed
+// before its first use) or, when ws is NULL, in split_scratch.  Internal
+// entry of cia_attn_decode_split(_ws) for nsplit <= kSplitMfmaMax
+// (arguments checked there).
 extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
     const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
     const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail, int committed, int qpos,
-    float scale, float* pm, float* pl, float* po, int nsplit, void* stream) {
+    float scale, float* pm, float* pl, float* po, int nsplit, void* ws, void* stream) {
   const int total = qpos + 1, chunk = (total + nsplit - 1) / nsplit;
   // workgroups per kv head: up to one per 8 CUs; fewer splits than that
   // are each spread over sub workgroups
@@ -1554,9 +1583,8 @@ extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
       da.rp[0] = 0;
     }
   }
-  void* ws = nullptr;
-  if (sub > 1 || sub < 0) {
-    const int st = split_ws_for_stream(&ws, (hipStream_t)stream);
+  if ((sub > 1 || sub < 0) && !ws) {
+    const int st = split_scratch_prepare((hipStream_t)stream);
     if (st) return st;
   }
   da.q = q;

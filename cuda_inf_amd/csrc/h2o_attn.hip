@@ -101,10 +101,18 @@ struct H2oPlace {
   int32_t* dst;  // dst[0] = the slot, -1 when none can be taken
   int n0, C, W, posj;
   // the previous step's mass launch's keys of this step's buffer (nkw
-  // pairs), or null: then every workgroup reads all masses and positions
+  // pairs), or null: then every workgroup reads all masses and positions.
+  // The keys are used only when the tag the mass launch stored beside them
+  // (keys[kKeyTag], keys[kKeyTag + 1]) equals (tag0, tag1): this buffer's
+  // attn_sum address and posj; else (a workspace shared with another layer,
+  // or a step in between) every slot is read.
   const uint64_t* keys;
   int nkw;
+  uint64_t tag0, tag1;
 };
+// index of the tag in the keys region, after the keys of up to 256 slot
+// workgroups x 4 waves (kMassMaxWg)
+constexpr int kKeyTag = 256 * 4 * 2;
 
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -153,7 +161,9 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
   if constexpr (kPlace) {
     tk = h2f(pl.k[kvh * D + lane]);
     tv = h2f(pl.v[kvh * D + lane]);
-    if (pl.n0 >= pl.C && pl.keys) {
+    const bool use_keys = pl.n0 >= pl.C && pl.keys && pl.keys[kKeyTag] == pl.tag0 &&
+                          pl.keys[kKeyTag + 1] == pl.tag1;
+    if (use_keys) {
       for (int x = tid; x < pl.nkw; x += 256) {
         kwin = min_u64(kwin, pl.keys[2 * x]);
         kall = min_u64(kall, pl.keys[2 * x + 1]);
@@ -520,6 +530,11 @@ __global__ __launch_bounds__(1024) void k_h2o_mass(H2oArgs a, int nsw) {
     }
     __syncthreads();
   }
+  if (a.keys && blockIdx.x == 0 && tid == 0) {
+    // the tag of these keys: this buffer, for a next step at posj + 1
+    a.keys[kKeyTag] = (uint64_t)(uintptr_t)a.attn_sum;
+    a.keys[kKeyTag + 1] = (uint64_t)(a.posj + 1);
+  }
   if (a.keys && wv < 4) {
     // each slot-owning wave's minimum keys
     kwin = wave_min_u64(kwin);
@@ -538,7 +553,8 @@ int64_t h2o_keys_offset(int S, int C) {
 }
 
 int64_t h2o_ws_bytes(int S, int C) {
-  return h2o_keys_offset(S, C) + (int64_t)kMassMaxWg * 4 * 2 * sizeof(uint64_t);
+  static_assert(kKeyTag == kMassMaxWg * 4 * 2, "key tag index");
+  return h2o_keys_offset(S, C) + (int64_t)(kKeyTag + 2) * sizeof(uint64_t);
 }
 
 }  // namespace cia
@@ -591,7 +607,7 @@ extern "C" int cia_attention_h2o(const uint16_t* q, const uint8_t* kf, const uin
     a.klim = 0;
     hipLaunchKernelGGL(k_h2o_scores<false>, dim3(nblk, NKV, sq), dim3(256), 0, s, a,
                        H2oPlace{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                nullptr, nullptr, 0, 0, 0, 0, nullptr, 0});
+                                nullptr, nullptr, 0, 0, 0, 0, nullptr, 0, 0, 0});
     int st = launch_status();
     if (st) return st;
     const int nsw = std::min((n_live + 255) / 256, kMassMaxWg);
@@ -656,7 +672,8 @@ extern "C" __attribute__((visibility("hidden"))) int cia_h2o_decode_step(
   const H2oPlace pl{k,  v,  kf, vf, ks,   vs,
                     attn_sum, slot_pos, dst_slots, n0, C, W, past,
                     keys_valid && n0 >= C ? keys : nullptr,
-                    4 * std::min((n0 + 255) / 256, kMassMaxWg)};
+                    4 * std::min((n0 + 255) / 256, kMassMaxWg),
+                    (uint64_t)(uintptr_t)attn_sum, (uint64_t)past};
   hipLaunchKernelGGL(k_h2o_scores<true>, dim3(nblk, NKV, 1), dim3(256), 0, s, a, pl);
   int st = launch_status();
   if (st) return st;

@@ -135,8 +135,8 @@ __device__ __forceinline__ int append_tail_src(int r, const AppendShape& sh) {
 // grid = (1 + nfull, 8 kv heads), block = 256.  Workgroup (0, h) also
 // writes kv head h's tail rows, after its own reads of the old ones (the
 // only reads of the tail in the launch), so no second launch is needed.
-__global__ __launch_bounds__(256) void k_append_commit(const uint16_t* __restrict__ ktail,
-                                                       const uint16_t* __restrict__ vtail,
+__global__ __launch_bounds__(256) void k_append_commit(uint16_t* __restrict__ ktail,
+                                                       uint16_t* __restrict__ vtail,
                                                        const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v,
                                                        uint8_t* __restrict__ kc8,

@@ -95,15 +95,29 @@ def attention_fused_fp8(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, out
 
 
 def attn_decode_split(q, kc8, vc8, ksc, vsc, ktail, vtail, committed: int, qpos: int,
-                      scale: float, pm, pl, po, nsplit: int = NSPLIT_DEFAULT) -> None:
-    """engine.cu:396-464 with a runtime split count."""
-    call("cia_attn_decode_split", _dev(q, "q", _F16, NH * D),
-         _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
-         _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
-         _dev(ktail, "ktail", _F16, KVGROUP * NKV * D), _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
-         committed, qpos, float(scale),
-         _dev(pm, "pm", (torch.float32,), NH * nsplit), _dev(pl, "pl", (torch.float32,), NH * nsplit),
-         _dev(po, "po", (torch.float32,), NH * nsplit * D), nsplit, _stream())
+                      scale: float, pm, pl, po, nsplit: int = NSPLIT_DEFAULT, ws=None) -> None:
+    """engine.cu:396-464 with a runtime split count.  ws (optional): a
+    workspace of split_workspace_bytes(nsplit) bytes, zeroed before its first
+    use, in place of the library's fixed device array."""
+    args = (_dev(q, "q", _F16, NH * D),
+            _dev(kc8, "kc8", (torch.uint8,)), _dev(vc8, "vc8", (torch.uint8,)),
+            _dev(ksc, "ksc", _F16), _dev(vsc, "vsc", _F16),
+            _dev(ktail, "ktail", _F16, KVGROUP * NKV * D),
+            _dev(vtail, "vtail", _F16, KVGROUP * NKV * D),
+            committed, qpos, float(scale),
+            _dev(pm, "pm", (torch.float32,), NH * nsplit),
+            _dev(pl, "pl", (torch.float32,), NH * nsplit),
+            _dev(po, "po", (torch.float32,), NH * nsplit * D), nsplit)
+    if ws is None:
+        call("cia_attn_decode_split", *args, _stream())
+    else:
+        call("cia_attn_decode_split_ws", *args,
+             _dev(ws, "ws", (torch.uint8,), split_workspace_bytes(nsplit)), ws.numel(), _stream())
+
+
+def split_workspace_bytes(nsplit: int) -> int:
+    """Workspace bytes of attn_decode_split's caller-workspace form."""
+    return int(_lib.lib().cia_split_workspace_bytes(nsplit))
 
 
 def attn_decode_combine(pm, pl, po, out, nsplit: int = NSPLIT_DEFAULT) -> None:

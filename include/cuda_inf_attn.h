@@ -16,7 +16,11 @@
  *   - All pointers are device pointers owned by the caller (hipMalloc'd),
  *     except where "host" is stated.  No entry point allocates device
  *     memory or synchronises: every call is enqueued on `stream`
- *     (a hipStream_t; NULL is the null stream).
+ *     (a hipStream_t; NULL is the null stream).  Two entry points use a
+ *     fixed device array inside the library instead of a workspace
+ *     argument (cia_attn_decode_split, cia_attn_decode_noalloc); calls of
+ *     them that overlap on one GPU race.  cia_weights_upload
+ *     (cuda_inf_model.h) is host I/O and allocates its pinned buffers.
  *   - Every entry point returns CIA_OK (0) or a cia_status code; none calls
  *     exit().  cia_strerror() names the code; after CIA_ERR_HIP,
  *     cia_last_hip_error() returns the hipError_t of the failing call.
@@ -136,15 +140,34 @@ int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
  * split writes m = -1e30, l = 0.  nsplit in [1, CIA_NSPLIT_MAX]
  * (the reference fixes 16).  With fewer splits than the launch has
  * workgroups per kv head, each split is shared by several workgroups that
- * meet in a device workspace the library allocates on the first call on a
- * stream (per device and stream, 750 KiB, kept until the process
- * ends): that first call is not capturable into a graph. */
+ * meet in a fixed device array inside the library (750 KiB per GPU, held
+ * until the process ends): the call allocates nothing and can be captured
+ * into a graph, the first call on a device included.  Calls on one GPU
+ * share that array, so calls that overlap on one GPU (several streams, or
+ * graph replays beside eager calls on another stream) race; such callers
+ * use cia_attn_decode_split_ws with a workspace per stream. */
 int cia_attn_decode_split(const uint16_t* q, const uint8_t* kc8,
                           const uint8_t* vc8, const uint16_t* ksc,
                           const uint16_t* vsc, const uint16_t* ktail,
                           const uint16_t* vtail, int committed, int qpos,
                           float scale, float* pm, float* pl, float* po,
                           int nsplit, void* stream);
+
+/* attn_decode_split (engine.cu:396-464) with a caller-owned workspace in
+ * place of the library's array, for callers that run split decodes on
+ * several streams at once: ws of ws_bytes >= cia_split_workspace_bytes(nsplit)
+ * bytes, 16-byte aligned, ZEROED before its first use (it holds arrival
+ * counters, which every call leaves at zero).  Calls that share a ws must
+ * not overlap.  Results are bit-identical to cia_attn_decode_split's. */
+int cia_attn_decode_split_ws(const uint16_t* q, const uint8_t* kc8,
+                             const uint8_t* vc8, const uint16_t* ksc,
+                             const uint16_t* vsc, const uint16_t* ktail,
+                             const uint16_t* vtail, int committed, int qpos,
+                             float scale, float* pm, float* pl, float* po,
+                             int nsplit, void* ws, int64_t ws_bytes,
+                             void* stream);
+/* workspace bytes of cia_attn_decode_split_ws (0 for nsplit < 1) */
+int64_t cia_split_workspace_bytes(int nsplit);
 
 /* attn_decode_combine (engine.cu:467-480; launch engine.cu:852).
  * Merges the nsplit partials of every query head into out [32][64] fp16;

@@ -278,3 +278,43 @@ def test_attention_h2o_kernel(orc, cia, dev, n_live, S, past, seed):
         i = int(np.argmax(got.view(np.uint32) != r_attn.view(np.uint32)))
         raise AssertionError(f"attn_sum differs at slot {i}: {got[i]!r} vs {r_attn[i]!r}")
     assert_close_f16(_u16(out), r32, what="attention_h2o")
+
+
+def test_h2o_layers_sharing_ws_mass(cia, dev):
+    """Two H2O layers that share one ws_mass, run through the decode loop:
+    each step's mass launch leaves the next step's placement keys in the
+    shared scratch, tagged with its layer's attn_sum and position, so the
+    other layer's scores launch sees a foreign tag and scans every slot.
+    Evictions, masses, positions, FP8 bytes and outputs are bit-identical
+    to the same two layers with a scratch each."""
+    import ctypes
+    from cuda_inf_amd import _lib
+    from cuda_inf_amd._lib import call
+    from cuda_inf_amd.layer import AttnLayer
+    from cuda_inf_amd.workload import qkv
+    C, W, P, N, nL = 256, 32, 256, 160, 2
+    q, k, v = qkv((P + N) * nL, seed=31, device="cpu", prep=False)
+    q = q.view(P + N, nL, 32, 64).to(dev)
+    k = k.view(P + N, nL, 8, 64).to(dev)
+    v = v.view(P + N, nL, 8, 64).to(dev)
+    runs = []
+    for shared in (False, True):
+        layers = [AttnLayer(P + N + 4, budget=C, window=W, prompt_len=P, max_batch=P, device=dev)
+                  for _ in range(nL)]
+        for l, L in enumerate(layers):
+            L.forward(q[:P, l].contiguous(), k[:P, l].contiguous(), v[:P, l].contiguous(), 0,
+                      evicted=False)
+        if shared:
+            layers[1]._s.ws_mass = layers[0].ws_mass.data_ptr()
+        arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+        out = torch.zeros((N, nL, 32, 64), dtype=torch.float16, device=dev)
+        call("cia_decode_loop", arr, nL, q[P].data_ptr(), k[P].data_ptr(), v[P].data_ptr(),
+             out.data_ptr(), P, N, 0.125, None, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        runs.append((layers, out))
+    (la, oa), (lb, ob) = runs
+    assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), "outputs differ"
+    for l in range(nL):
+        for name in ("hattn", "d_slotpos", "kf", "vf", "ks", "vs"):
+            x, y = getattr(la[l], name), getattr(lb[l], name)
+            assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), (l, name)
