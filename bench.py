@@ -91,7 +91,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
-    total_steps = W + 2 * K + a.cold_steps + a.prep_steps + a.block_steps + a.split_steps
+    total_steps = W + 3 * K + 2 + a.cold_steps + a.prep_steps + a.block_steps + a.split_steps
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
@@ -133,11 +133,14 @@ def main():
     qrow, krow = nL * NH * D, nL * NKV * D
     cur = {"step": 0}
 
-    def run(steps, events=None):
+    def run(steps, events=None, per=0):
+        """steps decode tokens through cia_decode_loop_ex: per = 0 runs the
+        layers of a token in one launch (k_decode_tok), 1 one launch per
+        layer (k_decode)"""
         s0 = cur["step"]
-        call("cia_decode_loop", arr, nL, q.data_ptr() + s0 * qrow * 2,
+        call("cia_decode_loop_ex", arr, nL, q.data_ptr() + s0 * qrow * 2,
              kk.data_ptr() + s0 * krow * 2, vv.data_ptr() + s0 * krow * 2,
-             out.data_ptr() + s0 * qrow * 2, ctx + s0, steps, 0.125, events,
+             out.data_ptr() + s0 * qrow * 2, ctx + s0, steps, 0.125, per, events,
              stream.cuda_stream)
         cur["step"] += steps
 
@@ -164,17 +167,18 @@ def main():
     timed_bytes = bytes_of_steps(s_timed, K)
     log(f"warm: {us_tok:.2f} us/token, effective {timed_bytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s")
 
-    # The decode launch (k_decode, one per layer: the FP8 stream, the tail,
-    # the fresh token's write and the merge) is the dominant work: its
-    # average duration is the timed region's span over its K * layers
+    # The decode launch (k_decode_tok, one per token for all nL layers: per
+    # layer the FP8 stream, the tail, the fresh token's write and the merge,
+    # layer l + 1 scored after layer l's output is stored) is the dominant
+    # work: its average duration is the timed region's span over its K
     # launches (events bracket the region on the kernels' own stream; 1 step
-    # in 64 also carries that layer's FP8 commit).
-    dec_us = warm_ms * 1e3 / (K * nL)
-    dec_bytes = timed_bytes / (K * nL)
+    # in 64 also carries every layer's FP8 commit).
+    dec_us = warm_ms * 1e3 / K
+    dec_bytes = timed_bytes / K
     achieved = dec_bytes / (dec_us * 1e-6) / 1e9
 
     # ---- the same launches one by one: HIP events recorded by the decode
-    # loop right before and after each layer's launch (each event adds its
+    # loop right before and after each token's launch (each event adds its
     # own marker overhead)
     nev = 3 * K * nL
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(nev)]
@@ -184,10 +188,27 @@ def main():
     ev_arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs]) if nev else None
     run(K, ev_arr)
     torch.cuda.synchronize()
-    one = sorted(evs[3 * r].elapsed_time(evs[3 * r + 1]) * 1e3 for r in range(K * nL))
+    one = sorted(evs[3 * nL * r].elapsed_time(evs[3 * nL * r + 1]) * 1e3 for r in range(K))
     ev_us = one[len(one) // 2]
-    log(f"decode launch: {dec_us:.2f} us per layer, {dec_bytes / 1e6:.2f} MB, {achieved:.0f} GB/s; "
-        f"event-bracketed median {ev_us:.2f} us")
+    log(f"decode launch: {dec_us:.2f} us per token ({nL} layers), {dec_bytes / 1e6:.2f} MB, "
+        f"{achieved:.0f} GB/s; event-bracketed median {ev_us:.2f} us")
+
+    # ---- the same tokens with one launch per layer (k_decode; the
+    # reference's per-layer launch structure)
+    run(2, per=1)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(K, per=1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pl_ms = e0.elapsed_time(e1)
+    pl_bytes = bytes_of_steps(cur["step"] - K, K)
+    per_layer = {"us_per_token": round(pl_ms * 1e3 / K, 3),
+                 "us_per_launch": round(pl_ms * 1e3 / (K * nL), 3),
+                 "gbps": round(pl_bytes / (pl_ms * 1e-3) / 1e9, 1),
+                 "kernel": "k_decode (one launch per layer)"}
+    log(f"one launch per layer: {per_layer['us_per_token']:.2f} us/token "
+        f"({per_layer['us_per_launch']:.2f} us per launch, {per_layer['gbps']:.0f} GB/s)")
 
     # ---- measured ceiling: a plain streaming read of the same layers'
     # committed FP8 K and V, one launch per layer, the same count of
@@ -211,7 +232,7 @@ def main():
     floor_bytes = 2 * arr[0].committed * NKV * D
     floor_gbps = floor_bytes / (floor_us * 1e-6) / 1e9
     log(f"plain read of the same bytes: {floor_us:.2f} us per layer, {floor_gbps:.0f} GB/s "
-        f"({dec_us / floor_us:.2f}x the decode launch's time)")
+        f"({dec_us / (nL * floor_us):.2f}x the decode's time)")
 
     # ---- cold: evict the KV from the 256 MB Infinity Cache before every token
     # by reading 1 GiB of other data (a read leaves no dirty lines behind)
@@ -548,7 +569,8 @@ def main():
         "data": "synthetic: seeded N(0,1), K/V 1% outliers x20, Q QK-RMSNorm+RoPE",
         "config": {"workload": f"flash-decoding, ctx {ctx}, {nL} attention layers/token, batch 1, "
                                f"32Q/8KV heads, d64, FP8 E4M3 group-64 KV + fp16 tail",
-                   "context": ctx, "layers": nL, "decode": "matrix-core, one launch per layer"
+                   "context": ctx, "layers": nL, "decode": "matrix-core, one launch per token "
+                   "(all layers; layer l+1 scored after layer l's output)"
                    if a.nsplit == 0 else f"split+combine nsplit={a.nsplit}"},
         "effective_gbps_warm": round(timed_bytes / (warm_ms * 1e-3) / 1e9, 1),
         "cold_us_per_token": round(cold_us, 3) if cold_us else None,
@@ -557,7 +579,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "traffic_source": TRAFFIC_FILE + " (not this run)" if traffic else None,
-                     "kernel": "k_decode (one launch per layer)",
+                     "kernel": f"k_decode_tok (one launch per token: {nL} layers)",
                      "algo_bytes_per_launch": int(dec_bytes),
                      "avg_launch_us": round(dec_us, 3),
                      "event_bracketed_median_us": round(ev_us, 3),
@@ -568,6 +590,7 @@ def main():
                          "frac": round(achieved / floor_gbps, 4),
                          "cold_us_per_token": round(floor_cold_us, 3) if floor_cold_us else None,
                          "cold_frac": round(floor_cold_us / cold_us, 4) if floor_cold_us else None}},
+        "per_layer_launches": per_layer,
         "prefill": prefill,
         "split16": split16,
         "qk_producers_fused": prep,

@@ -63,6 +63,8 @@ SIGNATURES = {
     "cia_layer_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
     "cia_layer_append": (_I, [_P, _P, _P, _I, _I, _P]),
     "cia_decode_loop": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
+    "cia_decode_loop_ex": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _I, _P, _P]),
+    "cia_decode_fault": (_I, [_P, ctypes.c_int64, _P]),
     # include/cuda_inf_model.h
     "cia_index_read": (_I, [ctypes.c_char_p, _P, ctypes.c_int64, _P]),
     "cia_file_size": (_I, [ctypes.c_char_p, _P]),
@@ -85,6 +87,20 @@ class CiaError(RuntimeError):
 
 
 _lib = None
+
+
+def use_timeline_build() -> None:
+    """Load libcuda_inf_attn_tl.so (``make -C cuda_inf_amd/csrc TIMELINE=1``:
+    the same library with per-wave timestamps in the one-launch decode)
+    instead of the product library.  Must be called before the first lib();
+    raises if that build is missing."""
+    global LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("the library is already loaded")
+    tl = os.path.join(HERE, "libcuda_inf_attn_tl.so")
+    if not os.path.exists(tl):
+        raise RuntimeError(f"{tl} is missing: build it with `make -C {CSRC} TIMELINE=1`")
+    LIB_PATH = tl
 
 
 def build(force: bool = False) -> str:

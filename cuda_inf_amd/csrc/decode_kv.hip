@@ -69,18 +69,13 @@
 #include <utility>
 
 #include "attn_range.h"
+#include "decode_wave.h"
 #include "qk_prep.h"
 
 namespace cia {
 
-constexpr int kFpWaves = 8;                // FP8 waves per workgroup
 constexpr int kTailWaves = GQA;            // tail waves (workgroup of range 0)
 constexpr int kDecThreads = 64 * (kFpWaves + kTailWaves);
-constexpr int kMaxRanges = 44;             // workgroups per kv head (32 on average)
-constexpr int kBlkB = 16 * 64 + 16;        // 16 keys x 64 B + 16 B pad
-constexpr int kTileB = 4 * kBlkB;          // one 64-key group of one kv head
-constexpr int kHalfB = 2 * kTileB;         // K (or V) of a unit
-constexpr int kScaleB = 256;               // K (or V) scales of a unit: 64 dwords, 2 used
 // LDS arena (one object: with several, the compiler tracks the LDS DMA
 // conservatively and turns the exact waits below into waits for everything)
 constexpr int kLdsK = 0;                                  // [8 waves][kHalfB]
@@ -96,13 +91,6 @@ constexpr int kLdsX = (kLdsTicket + 16 + 127) / 128 * 128;
 constexpr int kLdsXS = kLdsX + 2 * kTileB;
 constexpr int kLdsBytes = kLdsXS + 2 * kScaleB;
 static_assert(kLdsBytes <= 160 * 1024, "LDS");
-constexpr int kPartRow = 4 + D;            // one head's partial: m, l, -, -, o[64]
-constexpr int kPartF = GQA * kPartRow;     // floats of one workgroup partial
-constexpr int kCntStride = 64;             // uint32 between the kv heads' counters (256 B)
-constexpr float kLog2e = 1.44269504088896340736f;
-constexpr float kLn2 = 0.69314718055994530942f;
-constexpr int64_t kPartBytes = (int64_t)NKV * kMaxRanges * kPartF * sizeof(float);
-constexpr int64_t kWsBytes = kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
 // the split entry's workspace: two share slots per (kv head, range), then the counters
 constexpr int64_t kSplitWsBytes = 2 * kPartBytes + (int64_t)NKV * kCntStride * sizeof(uint32_t);
 
@@ -114,73 +102,6 @@ constexpr int64_t kSplitWsBytes = 2 * kPartBytes + (int64_t)NKV * kCntStride * s
 // complete call leaves them at zero; calls that overlap on one GPU race.
 static __device__ __align__(256) uint8_t split_scratch[kSplitWsBytes];
 
-typedef int i32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void gbl_void_t;
-
-__device__ __forceinline__ f16x8 cvt8(uint32_t w0, uint32_t w1) {
-  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
-  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
-  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
-  const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
-  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// max / sum over the 16 lanes of one head (lane bits 2..5; bits 0, 1 = head)
-__device__ __forceinline__ float head_max(float v) {
-  v = __builtin_fmaxf(v, row_ror<4>(v));
-  v = __builtin_fmaxf(v, row_ror<8>(v));
-  return col4_max(v);
-}
-__device__ __forceinline__ float head_sum(float v) {
-  v += row_ror<4>(v);
-  v += row_ror<8>(v);
-  return col4_sum(v);
-}
-
-// ds_read_b64_tr_b8 (within each 16-lane block, lane i receives byte i mod 8
-// of the 8-byte rows addressed by lanes 2k + (i div 8), k = 0..7), issued as
-// inline assembly: the compiler treats the builtin as touching every LDS
-// byte a pending DMA may write and would wait for all of them.  The result is
-// used only after lds_wait4.
-template <int kOff>
-__device__ __forceinline__ u32x2 ds_read_tr8_at(const uint8_t* p) {
-  u32x2 v;
-  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2"
-               : "=v"(v)
-               : "v"((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p), "i"(kOff));
-  return v;
-}
-#define ds_read_tr8(p, off) ds_read_tr8_at<off>(p)
-// waits for the LDS reads above and ties their results to the wait, so no
-// use is scheduled before it
-__device__ __forceinline__ void lds_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-}
-
-// Publishing a partial to the other workgroups: its agent-coherent stores
-// (relaxed agent-scope atomics) are acknowledged -- vmcnt(0): a store's
-// count drops when the L2 of this XCD has written it through -- before the
-// caller's barrier and its relaxed ticket increment, which another
-// workgroup's coherent loads then follow.  The wait builtin has no memory
-// semantics for the compiler, so compiler-only fences (no instruction) keep
-// the stores above it and the ticket below it.
-__device__ __forceinline__ void stores_acked() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  asm volatile("" ::: "memory");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, 0x00020000);
-}
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t nrec) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, nrec, 0x00020000);
-}
-constexpr int kCoherent = 16;  // sc1: agent-scope coherent access (L2 write-through / miss)
 
 struct DecArgs {
   const uint16_t* q;     // [32][64], raw when prep.qw is set
@@ -1320,80 +1241,6 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
 
 using namespace cia;
 
-// compute units of the current device (0 if unknown)
-static int device_cus() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
-// workgroups per kv head: about two groups per FP8 wave, 1 or even, <= 32,
-// and at most one workgroup per compute unit over the 8 kv heads (a
-// workgroup fills a CU's LDS; the cap keeps the whole grid resident at once)
-static int dec_ranges(int ng) {
-  int R = (ng + 2 * kFpWaves - 1) / (2 * kFpWaves);
-  if (R <= 1) return 1;
-  R += R & 1;
-  int cap = kMaxRanges;
-  const int cus = device_cus();
-  if (cus > 0 && cus / NKV < cap) cap = (cus / NKV) & ~1;
-  if (cap < 2) return 1;
-  return R > cap ? cap : R;
-}
-
-// The head pair whose bytes sit at 384..511 of each 512-byte block of the
-// cache (kv heads 2p and 2p + 1 own bytes 128p .. 128p + 127 of a key's
-// 512-byte row).  Measured on MI355X with per-wave timestamps: the
-// workgroups reading that quarter get their first data 1-1.5 us later and
-// take about a third longer over the same bytes (stream ends 24.5 against
-// 18.5 us at 131072 keys), from HBM and from the Infinity Cache alike; the
-// slow heads move with the buffers' base address (bases 128 or 256 bytes
-// further on make heads 4-5 or 2-3 the slow pair instead of 6-7).  -1 when K and V disagree or a base
-// is not 128-byte aligned.
-static int slow_pair(const void* kc8, const void* vc8) {
-  const uintptr_t k = (uintptr_t)kc8 & 511, v = (uintptr_t)vc8 & 511;
-  if (k != v || (k & 127)) return -1;
-  return (int)(((384 - k) & 511) >> 7);
-}
-
-// Workgroups per head pair for R per kv head on average (4R units of two
-// workgroups), once the stream is long (2 or more two-group units per FP8
-// wave on average: a workgroup's time then follows its bytes, its waves
-// sharing the CU's bandwidth): the slow pair gets rs, the others
-// (4R - rs) / 3, with rs the feasible count that minimises the costliest
-// workgroup's groups weighed 7/5 for the slow pair.  Shorter streams, or no
-// slow pair: equal ranges (rp[0] = 0).
-static void pair_ranges(int ng, int R, int slow, DecArgs& da) {
-  da.rp[0] = 0;
-  if (slow < 0 || R < 8 || ng < 4 * kFpWaves * R) return;
-  int best_rs = R;
-  double best = 7.0 / R;
-  for (int rs = R + 3; rs <= kMaxRanges && 4 * R - rs >= 3; rs += 3) {
-    const int rf = (4 * R - rs) / 3;
-    const double c = std::max(5.0 / rf, 7.0 / rs);
-    if (c < best) {
-      best = c;
-      best_rs = rs;
-    }
-  }
-  if (best_rs == R) return;
-  const int rf = (4 * R - best_rs) / 3;
-  int acc = 0;
-  for (int p = 0; p < 4; p++) {
-    da.rp[p] = p == slow ? best_rs : rf;
-    da.nep[p] = std::min(std::max(ng - 16 * da.rp[p], 0), da.rp[p] - 1);
-    da.up[p] = acc;
-    acc += da.rp[p];
-  }
-  da.up[4] = acc;
-}
-
 extern "C" int64_t cia_decode_workspace_bytes(int max_tokens) {
   return max_tokens < 0 ? 0 : kWsBytes;
 }
@@ -1417,7 +1264,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_mfma(
   DecArgs da{q, (uint8_t*)kc8, (uint8_t*)vc8, (uint16_t*)ksc, (uint16_t*)vsc, ktail, vtail,
              knew, vnew, committed, qpos, scale, (float*)ws,
              (uint32_t*)((char*)ws + kPartBytes), out, ng, R, ne, {}, {}, {}, QkPrep{}};
-  pair_ranges(ng, R, slow_pair(kc8, vc8), da);
+  pair_ranges(ng, R, slow_pair(kc8, vc8), da.rp, da.up, da.nep);
   if (prep) da.prep = *(const QkPrep*)prep;
   hipStream_t s = (hipStream_t)stream;
   if (da.prep.qw)
@@ -1571,7 +1418,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_split_mfma(
   const int ng = committed / G;
   DecArgs da{};
   if (nsplit < cap && !(cap & 1) && ng >= cap) {
-    pair_ranges(ng, cap, slow_pair(kc8, vc8), da);
+    pair_ranges(ng, cap, slow_pair(kc8, vc8), da.rp, da.up, da.nep);
     int rmin = cap;
     if (da.rp[0] > 0)
       for (int p = 0; p < 4; p++) rmin = std::min(rmin, da.rp[p]);

@@ -31,6 +31,13 @@ extern "C" __attribute__((visibility("hidden"))) int cia_qk_prep_into(
     const uint16_t* q, const uint16_t* k, const uint16_t* qw, const uint16_t* kw, uint16_t* oq,
     uint16_t* ok, int pos0, int S, float eps, float theta, void* stream);
 
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok_fits(const cia_layer* L,
+                                                                          int nl, int past);
+
+extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok(
+    const cia_layer* L, int nl, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+    uint16_t* out, int past, float scale, void* stream);
+
 extern "C" __attribute__((visibility("hidden"))) const void* cia_qk_prep_desc(
     const uint16_t* qw, const uint16_t* kw, float eps, float theta);
 
@@ -314,29 +321,53 @@ extern "C" int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t*
   return S ? group64_append(L, k, v, S, past, stream) : CIA_OK;
 }
 
-extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
-                               const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
-                               int steps, float scale, void** events, void* stream) {
+extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_t* q,
+                                  const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
+                                  int steps, float scale, int layers_per_launch, void** events,
+                                  void* stream) {
   if (!layers || !q || !k || !v || !out) return CIA_ERR_NULL;
-  if (n_layers < 1 || steps < 0 || past < 0) return CIA_ERR_ARG;
+  if (n_layers < 1 || steps < 0 || past < 0 || layers_per_launch < 0) return CIA_ERR_ARG;
   for (int l = 0; l < n_layers; l++) {
     const int st = prep_check(&layers[l]);
     if (st) return st;
   }
+  const int per = layers_per_launch == 0 ? CIA_DECODE_MAX_LAYERS_PER_LAUNCH
+                                         : std::min(layers_per_launch, CIA_DECODE_MAX_LAYERS_PER_LAUNCH);
   const size_t qrow = (size_t)CIA_NH * CIA_HEAD_DIM, krow = (size_t)CIA_NKV * CIA_HEAD_DIM;
   hipStream_t s = (hipStream_t)stream;
   for (int i = 0; i < steps; i++) {
-    for (int l = 0; l < n_layers; l++) {
+    const int pos = past + i;
+    for (int l = 0; l < n_layers;) {
       const size_t r = (size_t)i * n_layers + l;
-      cia_layer* L = &layers[l];
-      const int pos = past + i;
       int st;
+      // the next layers of this step in one launch, when they qualify
+      const int chunk = std::min(per, n_layers - l);
+      if (per > 1 && cia_decode_tok_fits(&layers[l], chunk, pos)) {
+        if (events)
+          for (int j = 0; j < chunk; j++)
+            if ((st = hip_check(hipEventRecord((hipEvent_t)events[3 * (r + j)], s)))) return st;
+        st = cia_decode_tok(&layers[l], chunk, q + r * qrow, k + r * krow, v + r * krow,
+                            out + r * qrow, pos, scale, stream);
+        if (st) return st;
+        if (events)
+          for (int j = 0; j < chunk; j++)
+            for (int e = 1; e < 3; e++)
+              if ((st = hip_check(hipEventRecord((hipEvent_t)events[3 * (r + j) + e], s)))) return st;
+        for (int j = 0; j < chunk; j++) {
+          cia_layer* Lj = &layers[l + j];
+          if (pos - Lj->committed == CIA_KVGROUP - 1) Lj->committed += CIA_KVGROUP;
+        }
+        l += chunk;
+        continue;
+      }
+      cia_layer* L = &layers[l];
       if (L->budget > 0) {
         if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r], s)))) return st;
         st = h2o_forward(L, q + r * qrow, k + r * krow, v + r * krow, out + r * qrow, 1, pos,
                          scale, nullptr, stream, events ? events[3 * r + 1] : nullptr, i > 0);
         if (st) return st;
         if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
+        l++;
         continue;
       }
       const bool fused = fused_append_ok(L, pos);
@@ -354,9 +385,17 @@ extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* 
                  : group64_attend(L, qi, out + r * qrow, 1, pos, scale, stream, mid);
       if (st) return st;
       if (events && (st = hip_check(hipEventRecord((hipEvent_t)events[3 * r + 2], s)))) return st;
+      l++;
     }
   }
   return CIA_OK;
+}
+
+extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
+                               const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
+                               int steps, float scale, void** events, void* stream) {
+  return cia_decode_loop_ex(layers, n_layers, q, k, v, out, past, steps, scale, 0, events,
+                            stream);
 }
 
 // ---------------------------------------------------------------- attention branch

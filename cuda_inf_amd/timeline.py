@@ -1,0 +1,122 @@
+"""Per-wave timeline of the one-launch decode (k_decode_tok) at the bench's
+decode workload: 6 layers, 32 768 tokens of context, fresh tokens appended
+one per step.  Uses the timestamp build (make -C cuda_inf_amd/csrc
+TIMELINE=1 -> libcuda_inf_attn_tl.so); each token's launch is synchronised
+and its stamps read back (s_memrealtime, 100 MHz), then medians over the
+tokens of each event's time since the launch's first wave started.
+
+    python -m cuda_inf_amd.timeline [--ctx 32768] [--layers 6] [--tokens 32]
+
+Printed per layer: the FP8 waves' "opened" (B1 passed), first unit's K
+landed, V landed, units done and partials-in-LDS (B2); the merge waves'
+partial acknowledged, ticket, final rows fetched (last arrivers) and output
+counted; the control wave's wait begun and q loaded.  Each as median / max
+over waves (median over tokens), in microseconds.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import statistics as st
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=6)
+    ap.add_argument("--tokens", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    a = ap.parse_args()
+    from cuda_inf_amd import _lib
+    _lib.use_timeline_build()
+    import numpy as np
+    import torch
+    from cuda_inf_amd import workload
+    from cuda_inf_amd._lib import D, NH, NKV, call
+    from cuda_inf_amd.layer import AttnLayer
+    lib = _lib.lib()
+    lib.cia_timeline_read.restype = ctypes.c_int
+    lib.cia_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    dev = torch.device("cuda:0")
+    s = torch.cuda.current_stream()
+    nL, ctx = a.layers, a.ctx
+    n = a.warmup + a.tokens
+    layers = []
+    for l in range(nL):
+        L = AttnLayer(ctx + n + 64, nsplit=0, device=dev)
+        g = workload.generator(1000 + l, dev)
+        for c0 in range(0, ctx, 8192):
+            m = min(8192, ctx - c0)
+            k = workload.with_outliers(workload.normal_f16((m, NKV, D), g, dev), g)
+            v = workload.with_outliers(workload.normal_f16((m, NKV, D), g, dev), g)
+            call("cia_layer_append", ctypes.byref(L._s), k.data_ptr(), v.data_ptr(), m, c0,
+                 s.cuda_stream)
+        layers.append(L)
+    torch.cuda.synchronize()
+    arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+    g = workload.generator(7, dev)
+    pos = torch.arange(ctx, ctx + n, device=dev)
+    q = workload.normal_f16((n, nL, NH, D), g, dev)
+    q = torch.stack([workload.prep_qk(q[:, l], pos) for l in range(nL)], dim=1).contiguous()
+    kk = workload.with_outliers(workload.normal_f16((n, nL, NKV, D), g, dev), g)
+    vv = workload.with_outliers(workload.normal_f16((n, nL, NKV, D), g, dev), g)
+    out = torch.empty((n, nL, NH, D), dtype=torch.float16, device=dev)
+    nwg_max, nw = 8 * 44, 13
+    buf = np.zeros(nwg_max * nw * 64, np.uint32)
+    qrow, krow = nL * NH * D * 2, nL * NKV * D * 2
+    samples = []
+    for i in range(n):
+        call("cia_decode_loop", arr, nL, q.data_ptr() + i * qrow, kk.data_ptr() + i * krow,
+             vv.data_ptr() + i * krow, out.data_ptr() + i * qrow, ctx + i, 1, 0.125, None,
+             s.cuda_stream)
+        torch.cuda.synchronize()
+        if i < a.warmup:
+            continue
+        _lib.check("cia_timeline_read", lib.cia_timeline_read(buf.ctypes.data, buf.nbytes))
+        samples.append(buf.reshape(nwg_max, nw, 64).copy())
+    ng = ctx // 64
+    R = min(32, ((ng + 15) // 16 + 1) // 2 * 2)
+    nwg = 8 * R
+    f = ctypes.c_int(-1)
+    call("cia_decode_fault", layers[0].ws_decode.data_ptr(), layers[0].ws_decode.numel(),
+         ctypes.byref(f))
+    print(f"timeline: ctx {ctx}, {nL} layers, {len(samples)} tokens, {nwg} workgroups; "
+          f"fault word {f.value}")
+
+    def rel(x, t0):
+        return ((x.astype(np.int64) - t0) % (1 << 32)) / 100.0  # us
+
+    rows = []
+    for smp in samples:
+        tl = smp[:nwg]
+        t0 = int(tl[:, :8, 63].min())
+        res = {}
+        for li in range(nL):
+            b = 8 * li
+            fp8 = rel(tl[:, :8, b:b + 5], t0)            # [wg][wave][5]
+            mw = rel(tl[:, 9:13, b:b + 6], t0)           # merge waves
+            ctl = rel(tl[:, 12, b + 6:b + 8], t0)        # control
+            res[(li, "fp8 opened")] = fp8[:, :, 0]
+            res[(li, "fp8 K landed")] = fp8[:, :, 1]
+            res[(li, "fp8 V landed")] = fp8[:, :, 2]
+            res[(li, "fp8 units done")] = fp8[:, :, 3]
+            res[(li, "partials in LDS")] = fp8[:, :, 4]
+            res[(li, "merge: partial acked")] = mw[:, :, 2]
+            res[(li, "merge: ticket")] = mw[:, :, 3]
+            last = tl[:, 9:13, b + 4] != 0
+            res[(li, "merge: final rows (last)")] = mw[:, :, 4][last] if last.any() else np.zeros(1)
+            res[(li, "merge: output counted (last)")] = mw[:, :, 5][last] if last.any() else np.zeros(1)
+            if li > 0:
+                res[(li, "control: wait begun")] = ctl[:, 0]
+            res[(li, "control: q loaded")] = ctl[:, 1]
+        rows.append(res)
+        buf[:] = 0
+    keys = list(rows[0].keys())
+    for key in keys:
+        med = st.median(float(np.median(r[key])) for r in rows)
+        mx = st.median(float(np.max(r[key])) for r in rows)
+        print(f"  layer {key[0]}  {key[1]:32s} median {med:7.2f}  max {mx:7.2f}")
+
+
+if __name__ == "__main__":
+    main()

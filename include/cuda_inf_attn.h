@@ -433,6 +433,36 @@ int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
                     int past, int steps, float scale, void** events,
                     void* stream);
 
+#define CIA_DECODE_MAX_LAYERS_PER_LAUNCH 8
+/* cia_decode_loop with the launch structure chosen: layers_per_launch 1
+ * runs every layer's attention in launches of its own (the reference's
+ * per-layer structure, engine.cu:846-852); 0 (cia_decode_loop's choice) or
+ * 2..8 runs up to that many consecutive layers of a step (at most
+ * CIA_DECODE_MAX_LAYERS_PER_LAUNCH) in ONE launch when they qualify: all on
+ * the group-64 cache with nsplit 0, the same committed count, the fresh
+ * token landing in each tail, the QK producers on all of them or none (one
+ * eps and theta), at least 8 committed groups per 64-key range of the
+ * launch (about 4096 keys and up), and a grid of one workgroup per compute
+ * unit that fits the device.  Otherwise the layer runs alone, as with 1.
+ * In one launch layer l + 1's scores start only after every output row of
+ * layer l is stored (its q would be computed from them), while its FP8 K/V
+ * already stream in; outputs and cache bytes are bit-identical to the
+ * per-layer launches.  The workspace is the first layer's ws_decode.  With
+ * events, every layer of such a launch has events[3r] recorded before it
+ * and events[3r+1], events[3r+2] after it.  The in-launch wait between
+ * layers is bounded: if the grid was not resident at once it gives up and
+ * sets the workspace's fault word (cia_decode_fault) rather than hang. */
+int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_t* q,
+                       const uint16_t* k, const uint16_t* v, uint16_t* out,
+                       int past, int steps, float scale,
+                       int layers_per_launch, void** events, void* stream);
+
+/* Reads (synchronously) the fault word of a decode workspace: nonzero when a
+ * one-launch multi-layer step gave up waiting for a previous layer (its
+ * outputs are then not valid).  The word stays set until the workspace is
+ * cleared.  No counterpart in the reference. */
+int cia_decode_fault(const void* ws, int64_t ws_bytes, int* fault);
+
 /* INT4 projection weights of one attention layer (the Q4 tensors
  * self_attn.{q,k,v,out}_proj.weight of engine.cu:792-797, 858) and the
  * scratch their outputs live in. */
