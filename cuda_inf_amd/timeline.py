@@ -26,6 +26,8 @@ def main():
     ap.add_argument("--layers", type=int, default=6)
     ap.add_argument("--tokens", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prep", action="store_true",
+                    help="raw q / k: the QK producers run inside the kernel")
     a = ap.parse_args()
     from cuda_inf_amd import _lib
     _lib.use_timeline_build()
@@ -54,6 +56,18 @@ def main():
         layers.append(L)
     torch.cuda.synchronize()
     arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+    keep = []
+    if a.prep:
+        g8 = workload.generator(17, dev)
+        qw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        kw = (1.0 + 0.1 * torch.randn(D, generator=g8, device=dev)).to(torch.float16)
+        keep += [qw, kw]
+        for l in range(nL):
+            pw = torch.zeros((NH + NKV) * D, dtype=torch.float16, device=dev)
+            keep.append(pw)
+            arr[l].qw, arr[l].kw = qw.data_ptr(), kw.data_ptr()
+            arr[l].eps, arr[l].theta = workload.EPS, workload.ROPE_THETA
+            arr[l].prep_ws, arr[l].prep_cap = pw.data_ptr(), 1
     g = workload.generator(7, dev)
     pos = torch.arange(ctx, ctx + n, device=dev)
     q = workload.normal_f16((n, nL, NH, D), g, dev)
@@ -111,6 +125,20 @@ def main():
             res[(li, "control: q loaded")] = ctl[:, 1]
         rows.append(res)
         buf[:] = 0
+    # the workgroup that reached "partials in LDS" last in each layer of
+    # the last token, with its waves' stamps of that layer
+    tl = samples[-1][:nwg]
+    t0 = int(tl[:, :8, 63].min())
+    for li in range(nL):
+        b = 8 * li
+        b2 = rel(tl[:, :8, b + 4], t0).max(axis=1)
+        wg = int(np.argmax(b2))
+        print(f"  layer {li}: last workgroup to B2: {wg} (xcd {wg % 8}, slot {wg // 8}) at "
+              f"{b2[wg]:.2f}; its waves (stamps 0..7 of the layer):")
+        for w in range(13):
+            st_ = rel(tl[wg, w, b:b + 8], t0)
+            st_[tl[wg, w, b:b + 8] == 0] = np.nan
+            print(f"    wave {w:2d}: " + " ".join(f"{x:7.2f}" for x in st_))
     keys = list(rows[0].keys())
     for key in keys:
         med = st.median(float(np.median(r[key])) for r in rows)
