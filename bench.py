@@ -469,7 +469,9 @@ def main():
                    "mfma_f16_frac": round(flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                    "kernel": "attention_fused",
                    "layer_us_with_append": round(lms * 1e3, 1),
-                   "fp8": {"kernel": "attention_fused_fp8 (v_mfma_scale_f32_16x16x128_f8f6f4)",
+                   "fp8_experimental": {
+                           "kernel": "attention_fused_fp8 (v_mfma_scale_f32_16x16x128_f8f6f4; "
+                                     "experimental, slower than the fp16 kernel, not on the path)",
                            "us": round(f8ms * 1e3, 1),
                            "tflops": round(flops / (f8ms * 1e-3) / 1e12, 2),
                            "mfma_fp8_frac": round(flops / (f8ms * 1e-3) / 1e12
@@ -477,8 +479,9 @@ def main():
                            "max_abs_diff_vs_fp16": round(float(d8.max()), 5),
                            "mean_abs_diff_vs_fp16": round(float(d8.mean()), 7)}}
         log(f"prefill {S}: attention {pms * 1e3:.1f} us, {prefill['tflops']} TFLOP/s; "
-            f"append + attention {lms * 1e3:.1f} us; fp8 {f8ms * 1e3:.1f} us "
-            f"({prefill['fp8']['tflops']} TFLOP/s), max |fp8 - fp16| {float(d8.max()):.4f}")
+            f"append + attention {lms * 1e3:.1f} us; experimental fp8 {f8ms * 1e3:.1f} us "
+            f"({prefill['fp8_experimental']['tflops']} TFLOP/s), "
+            f"max |fp8 - fp16| {float(d8.max()):.4f}")
         # the layer's INT4 projections over the S prompt rows (matrix-core
         # GEMM): q/k/v in one launch, out_proj into the residual
         H = _lib.HIDDEN

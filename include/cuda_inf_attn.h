@@ -119,13 +119,17 @@ int cia_attention_fused(const uint16_t* q, const uint8_t* kc8,
                         float* attn_sum, int S, int past, float scale,
                         void* ws, int64_t ws_bytes, void* stream);
 
-/* The causal attention of attention_fused (engine.cu:236-308) with both
- * products on the OCP-fp8 matrix cores (no counterpart kernel in the
- * reference; same arguments without attn_sum/ws).  K and V are used as the
- * cache's FP8 bytes; Q is quantised to fp8 per (query, head) with scale
+/* EXPERIMENTAL.  The causal attention of attention_fused (engine.cu:236-308)
+ * with both products on the OCP-fp8 matrix cores (no counterpart kernel in
+ * the reference; same arguments without attn_sum/ws).  K and V are used as
+ * the cache's FP8 bytes; Q is quantised to fp8 per (query, head) with scale
  * amax/448 and the softmax numerators per tile, so the output carries that
  * extra rounding: its error against the fp32 reference is reported, it is
- * not held to cia_attention_fused's tolerance. */
+ * not held to cia_attention_fused's tolerance.  On MI355X it is slower than
+ * cia_attention_fused (141-146 against 100-102 us at 4096 queries: the
+ * hi/lo terms that keep its error near fp16's double the contraction, and
+ * one fp8 term alone gives 0.09 max errors), so nothing in the library
+ * calls it; it is kept to measure the fp8 matrix cores against. */
 int cia_attention_fused_fp8(const uint16_t* q, const uint8_t* kc8,
                             const uint8_t* vc8, const uint16_t* ksc,
                             const uint16_t* vsc, const uint16_t* ktail,

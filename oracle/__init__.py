@@ -66,6 +66,7 @@ def _declare(L):
         "orc_kv_commit_group": (None, [_P, _P, _P, _P, _P, _P, _I, _I]),
         "orc_kv_append": (_I, [_P] * 8 + [_P, _I, _I]),
         "orc_attention_fused": (None, [_P] * 7 + [_I, _P, _P, _P, _I, _I, _F, _P, _I]),
+        "orc_attention_fused_mt": (None, [_P] * 7 + [_I, _P, _P, _I, _I, _F, _I, _I, _I]),
         "orc_attn_decode_split": (None, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I]),
         "orc_attn_decode_combine": (None, [_P, _P, _P, _P, _P, _I]),
         "orc_attn_decode_mt": (None, [_P] * 7 + [_I, _I, _F, _P, _P, _P, _I, _P, _P, _I]),
@@ -204,6 +205,19 @@ def attention_fused(q, cache: Group64Cache, S: int, past: int, scale: float = 0.
     r = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
     lib().orc_attention_fused(_p(q), *cache.ptrs(), cache.committed, _p(out16), _p(out32),
                               _p(attn_sum), S, past, scale, _p(r), 0 if r is None else r.size)
+    return out16, out32
+
+
+def attention_fused_mt(q, cache: Group64Cache, S: int, past: int, scale: float = 0.125,
+                       heads=(0, NH), nthreads: int = 1):
+    """attention_fused's outputs for query heads heads[0]..heads[1]-1 of all
+    S rows on nthreads threads (no attn_sum): identical per (row, head) to
+    attention_fused.  Returns (out16, out32) [S,NH,D]; other heads are 0."""
+    q = _u16(q)
+    out16 = np.zeros((S, NH, D), np.uint16)
+    out32 = np.zeros((S, NH, D), np.float32)
+    lib().orc_attention_fused_mt(_p(q), *cache.ptrs(), cache.committed, _p(out16), _p(out32),
+                                 S, past, scale, int(heads[0]), int(heads[1]), int(nthreads))
     return out16, out32
 
 

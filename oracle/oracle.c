@@ -452,6 +452,46 @@ ORC_HOT static void mass_from_scores(const float* s, const unsigned char* ok,
 /* ------------------------------------------------------------------ */
 /* attention_fused, engine.cu:236-308                                 */
 /* ------------------------------------------------------------------ */
+/* one (query i, head h) of attention_fused over the dequantised cache */
+static void fused_row_head(const uint16_t* q, const float* kd, const float* vd, int i, int h,
+                           int past, float scale, uint16_t* out16, float* out32, float* s) {
+  int qpos = past + i;
+  int kvh = h / GQA;
+  float qreg[D];
+  for (int d = 0; d < D; d++) qreg[d] = h2f(q[((size_t)i * NH + h) * D + d]);
+  /* one online-softmax pass in key order, fp32 (engine.cu:255-285) */
+  float m = -1e30f, l = 0.f, o[D];
+  for (int d = 0; d < D; d++) o[d] = 0.f;
+  for (int t = 0; t <= qpos; t++) {
+    const float* kr = kd + ((size_t)t * NKV + kvh) * D;
+    const float* vr = vd + ((size_t)t * NKV + kvh) * D;
+    float st = dot_chain(qreg, kr) * scale;
+    if (s) s[t] = st;
+    float mnew = fmaxf(m, st), c = expf(m - mnew), pe = expf(st - mnew);
+    l = fmaf(l, c, pe);
+    for (int d = 0; d < D; d++) o[d] = fmaf(pe, vr[d], o[d] * c);
+    m = mnew;
+  }
+  float inv = 1.f / l;
+  for (int d = 0; d < D; d++) {
+    float r = o[d] * inv;
+    size_t oi = ((size_t)i * NH + h) * D + d;
+    if (out32) out32[oi] = r;
+    if (out16) out16[oi] = orc_f32_to_f16(r);
+  }
+}
+
+/* the cache's keys 0..T-1 dequantised, [t][kv head][d] */
+static void dequant_cache(const uint8_t* kc8, const uint8_t* vc8, const uint16_t* ksc,
+                          const uint16_t* vsc, const uint16_t* ktail, const uint16_t* vtail,
+                          int committed, int T, float* kd, float* vd) {
+  for (int t = 0; t < T; t++)
+    for (int h = 0; h < NKV; h++) {
+      row_group64(kc8, ksc, ktail, committed, t, h, kd + ((size_t)t * NKV + h) * D);
+      row_group64(vc8, vsc, vtail, committed, t, h, vd + ((size_t)t * NKV + h) * D);
+    }
+}
+
 void orc_attention_fused(const uint16_t* q, const uint8_t* kc8,
                          const uint8_t* vc8, const uint16_t* ksc,
                          const uint16_t* vsc, const uint16_t* ktail,
@@ -460,14 +500,9 @@ void orc_attention_fused(const uint16_t* q, const uint8_t* kc8,
                          float scale, const int* rows, int n_rows) {
   int nq = rows ? n_rows : S;
   int T = past + S; /* keys 0..T-1 exist */
-  /* dequantised cache per kv head, both layouts: [t][d] and [d][t] */
   float* kd = (float*)malloc(sizeof(float) * (size_t)T * NKV * D);
   float* vd = (float*)malloc(sizeof(float) * (size_t)T * NKV * D);
-  for (int t = 0; t < T; t++)
-    for (int h = 0; h < NKV; h++) {
-      row_group64(kc8, ksc, ktail, committed, t, h, kd + ((size_t)t * NKV + h) * D);
-      row_group64(vc8, vsc, vtail, committed, t, h, vd + ((size_t)t * NKV + h) * D);
-    }
+  dequant_cache(kc8, vc8, ksc, vsc, ktail, vtail, committed, T, kd, vd);
   float* s = (float*)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
   float* e = (float*)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
   float* p = (float*)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
@@ -476,29 +511,7 @@ void orc_attention_fused(const uint16_t* q, const uint8_t* kc8,
     int i = rows ? rows[qi] : qi;
     int qpos = past + i;
     for (int h = 0; h < NH; h++) {
-      int kvh = h / GQA;
-      float qreg[D];
-      for (int d = 0; d < D; d++) qreg[d] = h2f(q[((size_t)i * NH + h) * D + d]);
-      /* one online-softmax pass in key order, fp32 (engine.cu:255-285) */
-      float m = -1e30f, l = 0.f, o[D];
-      for (int d = 0; d < D; d++) o[d] = 0.f;
-      for (int t = 0; t <= qpos; t++) {
-        const float* kr = kd + ((size_t)t * NKV + kvh) * D;
-        const float* vr = vd + ((size_t)t * NKV + kvh) * D;
-        float st = dot_chain(qreg, kr) * scale;
-        s[t] = st;
-        float mnew = fmaxf(m, st), c = expf(m - mnew), pe = expf(st - mnew);
-        l = fmaf(l, c, pe);
-        for (int d = 0; d < D; d++) o[d] = fmaf(pe, vr[d], o[d] * c);
-        m = mnew;
-      }
-      float inv = 1.f / l;
-      for (int d = 0; d < D; d++) {
-        float r = o[d] * inv;
-        size_t oi = ((size_t)i * NH + h) * D + d;
-        if (out32) out32[oi] = r;
-        if (out16) out16[oi] = orc_f32_to_f16(r);
-      }
+      fused_row_head(q, kd, vd, i, h, past, scale, out16, out32, s);
       if (attn_sum) {
         for (int t = 0; t <= qpos; t++) ok[t] = 1;
         mass_from_scores(s, ok, qpos + 1, e, p);
@@ -507,6 +520,51 @@ void orc_attention_fused(const uint16_t* q, const uint8_t* kc8,
     }
   }
   free(kd); free(vd); free(s); free(e); free(p); free(ok);
+}
+
+/* attention_fused's outputs (no attn_sum) for query heads [h0, h1) of every
+ * row, rows dealt round-robin to nthreads threads; each (row, head) is the
+ * same computation as orc_attention_fused's, so the results are identical */
+struct fused_job {
+  const uint16_t* q;
+  const float* kd;
+  const float* vd;
+  uint16_t* out16;
+  float* out32;
+  int S, past, h0, h1, nthreads, tix;
+  float scale;
+};
+
+static void* fused_worker(void* arg) {
+  struct fused_job* j = (struct fused_job*)arg;
+  for (int i = j->tix; i < j->S; i += j->nthreads)
+    for (int h = j->h0; h < j->h1; h++)
+      fused_row_head(j->q, j->kd, j->vd, i, h, j->past, j->scale, j->out16, j->out32, NULL);
+  return NULL;
+}
+
+void orc_attention_fused_mt(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                            const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
+                            const uint16_t* vtail, int committed, uint16_t* out16, float* out32,
+                            int S, int past, float scale, int h0, int h1, int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > 256) nthreads = 256;
+  if (h0 < 0) h0 = 0;
+  if (h1 > NH) h1 = NH;
+  int T = past + S;
+  float* kd = (float*)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1) * NKV * D);
+  float* vd = (float*)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1) * NKV * D);
+  dequant_cache(kc8, vc8, ksc, vsc, ktail, vtail, committed, T, kd, vd);
+  pthread_t th[256];
+  struct fused_job jobs[256];
+  for (int i = 0; i < nthreads; i++) {
+    struct fused_job jb = {q, kd, vd, out16, out32, S, past, h0, h1, nthreads, i, scale};
+    jobs[i] = jb;
+  }
+  for (int i = 1; i < nthreads; i++) pthread_create(&th[i], NULL, fused_worker, &jobs[i]);
+  fused_worker(&jobs[0]);
+  for (int i = 1; i < nthreads; i++) pthread_join(th[i], NULL);
+  free(kd); free(vd);
 }
 
 /* ------------------------------------------------------------------ */

@@ -108,6 +108,12 @@ void orc_attention_fused(const uint16_t* q, const uint8_t* kc8,
                          const uint16_t* vtail, int committed, uint16_t* out16,
                          float* out32, float* attn_sum, int S, int past,
                          float scale, const int* rows, int n_rows);
+/* orc_attention_fused's outputs for query heads [h0, h1) of all S rows on
+ * nthreads threads (no attn_sum); identical per (row, head) */
+void orc_attention_fused_mt(const uint16_t* q, const uint8_t* kc8, const uint8_t* vc8,
+                            const uint16_t* ksc, const uint16_t* vsc, const uint16_t* ktail,
+                            const uint16_t* vtail, int committed, uint16_t* out16, float* out32,
+                            int S, int past, float scale, int h0, int h1, int nthreads);
 
 /* engine.cu:396-464 with runtime nsplit (reference: NSPLIT=16) and the
  * reference's 128-thread block structure. */

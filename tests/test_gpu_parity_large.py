@@ -7,8 +7,8 @@
   32 768: every step's output within tolerance and the committed group and
   tail bytes identical, once with prepared q/k and once with the QK
   producers inside the decode kernel;
-- the reference's split + combine at 131 072 keys, 16 and 512 splits: the
-  output and the partials;
+- the reference's split + combine at 131 072 keys, 16, 64, 256 and 512
+  splits (the benchmark's sweep): the output and the partials;
 - one 4096-token append: every committed byte and scale and the tail.
 """
 import ctypes
@@ -204,7 +204,7 @@ def cache131k(orc, dev):
     return L, ref
 
 
-@pytest.mark.parametrize("nsplit", [16, 512])
+@pytest.mark.parametrize("nsplit", [16, 64, 256, 512])
 def test_split_combine_131k(orc, cia, dev, cache131k, nsplit):
     from cuda_inf_amd import kernels as K
     from cuda_inf_amd.workload import qkv

@@ -248,6 +248,23 @@ def test_decode_mt_equals_single_thread(orc):
     assert np.array_equal(a[1], b[1]) and np.array_equal(a[0], b[0])
 
 
+def test_fused_mt_equals_single_thread(orc):
+    """The threaded head-range form of attention_fused (the checker of the
+    4096-token prefill's every row) gives the single-threaded oracle's bits
+    for the heads it covers and leaves the others zero."""
+    rng = np.random.default_rng(23)
+    S, past = 90, 40
+    c, _, _ = make_cache(orc, rng, past + S)
+    q = rand_f16(rng, (S, NH, D))
+    a16, a32 = orc.attention_fused(bits(q), c, S, past)
+    b16, b32 = orc.attention_fused_mt(bits(q), c, S, past, heads=(8, 16), nthreads=5)
+    assert np.array_equal(b32[:, 8:16].view(np.uint32), a32[:, 8:16].view(np.uint32))
+    assert np.array_equal(b16[:, 8:16], a16[:, 8:16])
+    assert not b32[:, :8].any() and not b32[:, 16:].any()
+    c16, c32 = orc.attention_fused_mt(bits(q), c, S, past, nthreads=3)
+    assert np.array_equal(c32.view(np.uint32), a32.view(np.uint32))
+
+
 # ---------------------------------------------------------------- H2O
 def h2o_setup(orc, rng, C, W, n, prompt):
     q = rand_f16(rng, (n, NH, D))
