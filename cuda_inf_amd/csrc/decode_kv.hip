@@ -773,127 +773,132 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     const int tt = a.qpos + 1 - a.committed;  // tail keys (the fresh token last)
     const bool fresh = a.knew != nullptr;
     const bool commit = fresh && tt == G;
-    if (fresh && i == 0) {
-      // the fresh token: k prepared when raw, kept in LDS for the scores and
-      // written into its tail row with v (engine.cu:190-198)
-      const uint16_t kraw = a.knew[g * D + l];
-      uint16_t kv;
-      if constexpr (kPrep)
-        kv = qk_norm_rope_lane(h2f(kraw), h2f(a.prep.kw[l]), l, a.qpos, a.prep.eps, a.prep.rt);
-      else
-        kv = kraw;
-      skn[l] = kv;
-      a.ktail[((size_t)(tt - 1) * NKV + g) * D + l] = kv;
-      a.vtail[((size_t)(tt - 1) * NKV + g) * D + l] = a.vnew[g * D + l];
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();  // B1: q rows and the fresh k in LDS
-    // ---- scores: lane = key
-    const bool live = l < tt;
-    const int krow = live ? l : 0;  // (tail row 0 exists whatever the tail length)
-    const uint16_t* kp = a.ktail + ((size_t)krow * NKV + g) * D;
-    u32x4 kq[8], qq[8];
-#pragma unroll
-    for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(kp + 8 * cc);
-#pragma unroll
-    for (int cc = 0; cc < 8; cc++) qq[cc] = *(const u32x4*)(sq + i * D + 8 * cc);
-    if (fresh && l == tt - 1) {
-#pragma unroll
-      for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(skn + 8 * cc);
-    }
-    float x;
-    if (!commit) {
-      float sacc = 0.f;
-#pragma unroll
-      for (int cc = 0; cc < 8; cc++) {
-        const f16x8 q8 = __builtin_bit_cast(f16x8, qq[cc]), k8 = __builtin_bit_cast(f16x8, kq[cc]);
-        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 0, 1), __builtin_shufflevector(k8, k8, 0, 1), sacc, false);
-        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 2, 3), __builtin_shufflevector(k8, k8, 2, 3), sacc, false);
-        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 4, 5), __builtin_shufflevector(k8, k8, 4, 5), sacc, false);
-        sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 6, 7), __builtin_shufflevector(k8, k8, 6, 7), sacc, false);
+    const int nold = fresh ? tt - 1 : tt;  // rows already in the tail buffer
+    // (the step that commits the group and the others in separate code:
+    // their registers never meet)
+    auto tail_wave = [&](auto commit_tag) __attribute__((always_inline)) {
+      constexpr bool kCommit = decltype(commit_tag)::value;
+      // the old rows in one batch (tail_k_load / tail_v_load: rows from
+      // nold on read as zero), before B1; on the committing step the V rows
+      // load after the scores (the K quantisation needs the registers)
+      u32x4 kq[8], qq[8];
+      uint32_t vr[G / 2];
+      tail_k_load(a.ktail, g, nold, kq);
+      if constexpr (!kCommit) tail_v_load(a.vtail, g, nold, vr);
+      const uint32_t fv = fresh ? *(const uint32_t*)(a.vnew + g * D + 2 * (l & 31)) : 0u;
+      if (fresh && i == 0) {
+        // the fresh token: k prepared when raw, kept in LDS for the scores and
+        // written into its tail row with v (engine.cu:190-198)
+        const uint16_t kraw = a.knew[g * D + l];
+        uint16_t kv;
+        if constexpr (kPrep)
+          kv = qk_norm_rope_lane(h2f(kraw), h2f(a.prep.kw[l]), l, a.qpos, a.prep.eps, a.prep.rt);
+        else
+          kv = kraw;
+        skn[l] = kv;
+        a.ktail[((size_t)(tt - 1) * NKV + g) * D + l] = kv;
+        a.vtail[((size_t)(tt - 1) * NKV + g) * D + l] = a.vnew[g * D + l];
       }
-      x = sacc * qscale;
-    } else {
-      // The fresh token fills the group: kv_commit_group (engine.cu:202-228)
-      // of kv head g, and the group is attended in its FP8 form.  Lane l
-      // quantises key l; wave 0 writes the bytes and the scale.
-      float kf[D];
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();  // B1: q rows and the fresh k in LDS
+      // ---- scores: lane = key
+      const bool live = l < tt;
 #pragma unroll
-      for (int cc = 0; cc < 8; cc++)
+      for (int cc = 0; cc < 8; cc++) qq[cc] = *(const u32x4*)(sq + i * D + 8 * cc);
+      if (fresh && l == tt - 1) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          kf[8 * cc + 2 * e] = h2f((uint16_t)kq[cc][e]);
-          kf[8 * cc + 2 * e + 1] = h2f((uint16_t)(kq[cc][e] >> 16));
+        for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(skn + 8 * cc);
+      }
+      float x;
+      if constexpr (!kCommit) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < 8; cc++) {
+          const f16x8 q8 = __builtin_bit_cast(f16x8, qq[cc]), k8 = __builtin_bit_cast(f16x8, kq[cc]);
+          sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 0, 1), __builtin_shufflevector(k8, k8, 0, 1), sacc, false);
+          sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 2, 3), __builtin_shufflevector(k8, k8, 2, 3), sacc, false);
+          sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 4, 5), __builtin_shufflevector(k8, k8, 4, 5), sacc, false);
+          sacc = __builtin_amdgcn_fdot2(__builtin_shufflevector(q8, q8, 6, 7), __builtin_shufflevector(k8, k8, 6, 7), sacc, false);
         }
-      float ak = 0.f;
+        x = sacc * qscale;
+      } else {
+        // The fresh token fills the group: kv_commit_group (engine.cu:202-228)
+        // of kv head g, and the group is attended in its FP8 form.  Lane l
+        // quantises key l; wave 0 writes the bytes and the scale.
+        float kf[D];
 #pragma unroll
-      for (int d = 0; d < D; d++) ak = __builtin_fmaxf(ak, __builtin_fabsf(kf[d]));
-      const float sck = quant_scale(wave_max_fast(ak));
-      const uint16_t skh = f2h(sck);
-      const float kdq = h2f(skh);
-      uint8_t* krow8 = a.kc8 + ((size_t)(a.committed + l) * NKV + g) * D;
-      float sacc = 0.f;
+        for (int cc = 0; cc < 8; cc++)
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const uint32_t kb = e4m3x4(kf[4 * j] / sck, kf[4 * j + 1] / sck, kf[4 * j + 2] / sck,
-                                   kf[4 * j + 3] / sck);
-        const f16x8 q8 = __builtin_bit_cast(f16x8, qq[j >> 1]);
-        const int o4 = (j & 1) * 4;
-        sacc = __builtin_fmaf((float)q8[o4 + 0], e4m3_to_f32<0>(kb) * kdq, sacc);
-        sacc = __builtin_fmaf((float)q8[o4 + 1], e4m3_to_f32<1>(kb) * kdq, sacc);
-        sacc = __builtin_fmaf((float)q8[o4 + 2], e4m3_to_f32<2>(kb) * kdq, sacc);
-        sacc = __builtin_fmaf((float)q8[o4 + 3], e4m3_to_f32<3>(kb) * kdq, sacc);
-        if (i == 0) *(uint32_t*)(krow8 + 4 * j) = kb;
-      }
-      if (i == 0 && l == 0) a.ksc[(a.committed / G) * NKV + g] = skh;
-      x = sacc * qscale;
-    }
-    x = live ? x : -1e30f;
-    const float M = wave_max_fast(x);
-    const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
-    const float L = wave_sum_fast(p);
-    // ---- P V: lane = dim; V rows of the tail (the fresh row from vnew)
-    float o = 0.f;
-    if (!commit) {
-      for (int k0 = 0; k0 < tt; k0 += 16) {
-        float vv[16];
+          for (int e = 0; e < 4; e++) {
+            kf[8 * cc + 2 * e] = h2f((uint16_t)kq[cc][e]);
+            kf[8 * cc + 2 * e + 1] = h2f((uint16_t)(kq[cc][e] >> 16));
+          }
+        float ak = 0.f;
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int k = k0 + e < tt ? k0 + e : 0;
-          const uint16_t* vp = (fresh && k == tt - 1) ? a.vnew + g * D : a.vtail + ((size_t)k * NKV + g) * D;
-          vv[e] = h2f(vp[l]);
+        for (int d = 0; d < D; d++) ak = __builtin_fmaxf(ak, __builtin_fabsf(kf[d]));
+        const float sck = quant_scale(wave_max_fast(ak));
+        const uint16_t skh = f2h(sck);
+        const float kdq = h2f(skh);
+        uint8_t* krow8 = a.kc8 + ((size_t)(a.committed + l) * NKV + g) * D;
+        float sacc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const uint32_t kb = e4m3x4(kf[4 * j] / sck, kf[4 * j + 1] / sck, kf[4 * j + 2] / sck,
+                                     kf[4 * j + 3] / sck);
+          const f16x8 q8 = __builtin_bit_cast(f16x8, qq[j >> 1]);
+          const int o4 = (j & 1) * 4;
+          sacc = __builtin_fmaf((float)q8[o4 + 0], e4m3_to_f32<0>(kb) * kdq, sacc);
+          sacc = __builtin_fmaf((float)q8[o4 + 1], e4m3_to_f32<1>(kb) * kdq, sacc);
+          sacc = __builtin_fmaf((float)q8[o4 + 2], e4m3_to_f32<2>(kb) * kdq, sacc);
+          sacc = __builtin_fmaf((float)q8[o4 + 3], e4m3_to_f32<3>(kb) * kdq, sacc);
+          if (i == 0) *(uint32_t*)(krow8 + 4 * j) = kb;
         }
+        if (i == 0 && l == 0) a.ksc[(a.committed / G) * NKV + g] = skh;
+        x = sacc * qscale;
+      }
+      x = live ? x : -1e30f;
+      const float M = wave_max_fast(x);
+      const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
+      const float L = wave_sum_fast(p);
+      // ---- P V (tail_pv: rows summed per parity, then even + odd)
+      if constexpr (!kCommit) {
+        const f32x2 o = tail_pv(vr, p, fresh ? tt - 1 : -1, fv);
+        if (l < 32) *(f32x2*)(sO + (kFpWaves * GQA + i) * D + 2 * l) = o;
+      } else {
+        // the whole group (tt == 64): V quantised with its group scale;
+        // lane = dim, row 63 the fresh one; P V in tail_pv's order
+        float vv[G];
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k0 + e));
-          if (k0 + e < tt) o = __builtin_fmaf(pk, vv[e], o);
+        for (int k = 0; k < G; k++) {
+          const uint16_t* vp = k == G - 1 ? a.vnew + g * D : a.vtail + ((size_t)k * NKV + g) * D;
+          vv[k] = h2f(vp[l]);
         }
-      }
-    } else {
-      // the whole group (tt == 64): V quantised with its group scale
-      float vv[G];
+        float av = 0.f;
 #pragma unroll
-      for (int k = 0; k < G; k++) {
-        const uint16_t* vp = k == G - 1 ? a.vnew + g * D : a.vtail + ((size_t)k * NKV + g) * D;
-        vv[k] = h2f(vp[l]);
-      }
-      float av = 0.f;
+        for (int k = 0; k < G; k++) av = __builtin_fmaxf(av, __builtin_fabsf(vv[k]));
+        const float scv = quant_scale(wave_max_fast(av));
+        const uint16_t svh = f2h(scv);
+        const float vdq = h2f(svh);
+        float oe = 0.f, oo = 0.f;
 #pragma unroll
-      for (int k = 0; k < G; k++) av = __builtin_fmaxf(av, __builtin_fabsf(vv[k]));
-      const float scv = quant_scale(wave_max_fast(av));
-      const uint16_t svh = f2h(scv);
-      const float vdq = h2f(svh);
-#pragma unroll
-      for (int k = 0; k < G; k++) {
-        const uint32_t vb = e4m3x2(vv[k] / scv, 0.f) & 0xFFu;
-        if (i == 0) a.vc8[((size_t)(a.committed + k) * NKV + g) * D + l] = (uint8_t)vb;
-        const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
-        o = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, o);
+        for (int k = 0; k < G; k++) {
+          const uint32_t vb = e4m3x2(vv[k] / scv, 0.f) & 0xFFu;
+          if (i == 0) a.vc8[((size_t)(a.committed + k) * NKV + g) * D + l] = (uint8_t)vb;
+          const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
+          if (k & 1) oo = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, oo);
+          else oe = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, oe);
+        }
+        if (i == 0 && l == 0) a.vsc[(a.committed / G) * NKV + g] = svh;
+        sO[(kFpWaves * GQA + i) * D + l] = oe + oo;
       }
-      if (i == 0 && l == 0) a.vsc[(a.committed / G) * NKV + g] = svh;
-    }
-    sO[(kFpWaves * GQA + i) * D + l] = o;
-    if (l == 0) sml[kFpWaves * GQA + i] = f32x2{M, L};
+      if (l == 0) sml[kFpWaves * GQA + i] = f32x2{M, L};
+    };
+    using T_ = std::integral_constant<bool, true>;
+    using F_ = std::integral_constant<bool, false>;
+    if (commit)
+      tail_wave(T_{});
+    else
+      tail_wave(F_{});
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();  // B2: every wave's partial in LDS

@@ -360,7 +360,9 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     issue_scales(0, g0, sw);
     issue(a.L[0].kc8, g0, kw);
+    issue(a.L[0].vc8, g0, vw);
     __builtin_amdgcn_sched_barrier(0);
+    vpre = true;
   }
 
   // control wave: wait for layer li - 1, then layer li's q rows (and fresh token) into LDS
@@ -478,8 +480,20 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     }
     if (l < GQA) sml[pw * GQA + l] = f32x2{mx, lsum};
   };
-  // tail waves (range 0): layer li's fp16 tail, fresh token and commit
-  auto tail_layer = [&](int li) __attribute__((always_inline)) {
+  // tail waves (range 0): layer li's fp16 tail, fresh token and commit.
+  // tail_load runs before B1: the old rows of the kv head's tail into
+  // registers, K and V in one batch, so their round trip runs under the wait
+  // for the layer's q; the fresh row comes from LDS after B1.  On the step
+  // that commits the group the V rows load after the scores (the K
+  // quantisation needs the registers).
+  u32x4 tkq[8];
+  uint32_t tvr[G / 2];
+  auto tail_load = [&](int li, auto commit_tag) __attribute__((always_inline)) {
+    tail_k_load(a.L[li].ktail, g, tt - 1, tkq);
+    if constexpr (!decltype(commit_tag)::value) tail_v_load(a.L[li].vtail, g, tt - 1, tvr);
+  };
+  auto tail_layer = [&](int li, auto commit_tag) __attribute__((always_inline)) {
+    constexpr bool commit = decltype(commit_tag)::value;
     const TokLayer& Ly = a.L[li];
     const int i = w - kFpWaves;  // query head 4g + i
     if (i == 0) {
@@ -489,18 +503,16 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     }
     // ---- scores: lane = key (the fresh row from LDS); q from LDS as used
     const bool live = l < tt;
-    const int krow = live ? l : 0;  // (tail row 0 exists whatever the tail length)
-    const uint16_t* kp = Ly.ktail + ((size_t)krow * NKV + g) * D;
     const uint16_t* qrow = sq + i * D;
     u32x4 kq[8];
 #pragma unroll
-    for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(kp + 8 * cc);
+    for (int cc = 0; cc < 8; cc++) kq[cc] = tkq[cc];
     if (l == tt - 1) {
 #pragma unroll
       for (int cc = 0; cc < 8; cc++) kq[cc] = *(const u32x4*)(skn + 8 * cc);
     }
     float x;
-    if (!commit) {
+    if constexpr (!commit) {
       float sacc = 0.f;
 #pragma unroll
       for (int cc = 0; cc < 8; cc++) {
@@ -550,31 +562,15 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     const float M = wave_max_fast(x);
     const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
     const float L = wave_sum_fast(p);
-    // ---- P V: lane = dim; V rows of the tail (the fresh row from LDS)
-    float o = 0.f;
-    if (!commit) {
-      const uint16_t fresh_v = svn[l];
-      for (int k0 = 0; k0 < tt; k0 += 16) {
-        // (all 16 loads first, then a branch-free choice of the fresh row:
-        // one round trip per 16 rows)
-        uint16_t raw[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int k = k0 + e < tt - 1 ? k0 + e : 0;
-          raw[e] = Ly.vtail[((size_t)k * NKV + g) * D + l];
-        }
-        float vv[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) vv[e] = h2f(k0 + e == tt - 1 ? fresh_v : raw[e]);
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k0 + e));
-          if (k0 + e < tt) o = __builtin_fmaf(pk, vv[e], o);
-        }
-      }
+    // ---- P V (the fresh V row from LDS)
+    const uint32_t fv = *(const uint32_t*)(svn + 2 * (l & 31));
+    f32x2 o;
+    if constexpr (!commit) {
+      o = tail_pv(tvr, p, tt - 1, fv);
     } else {
-      // the whole group (tt == 64): V quantised with its group scale; the
-      // rows held two per register (row 2k low, 2k + 1 high)
+      // the whole group (tt == 64): V quantised with its group scale; lane =
+      // dim, the rows held two per register (row 2k low, 2k + 1 high), the
+      // fresh row 63 from LDS
       uint32_t vp[G / 2];
 #pragma unroll
       for (int k = 0; k < G / 2; k++) {
@@ -591,17 +587,25 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       const float scv = quant_scale(wave_max_fast(av));
       const uint16_t svh = f2h(scv);
       const float vdq = h2f(svh);
+      // P V in the order of tail_pv: even rows, odd rows, then their sum
+      float oe = 0.f, oo = 0.f;
 #pragma unroll
       for (int k = 0; k < G; k++) {
         const float vk = h2f((uint16_t)(vp[k >> 1] >> (16 * (k & 1))));
         const uint32_t vb = e4m3x2(vk / scv, 0.f) & 0xFFu;
         if (i == 0) Ly.vc8[((size_t)(committed + k) * NKV + g) * D + l] = (uint8_t)vb;
         const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
-        o = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, o);
+        if (k & 1) oo = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, oo);
+        else oe = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, oe);
       }
       if (i == 0 && l == 0) Ly.vsc[(committed / G) * NKV + g] = svh;
+      o = f32x2{oe + oo, 0.f};
     }
-    sO[(kFpWaves * GQA + i) * D + l] = o;
+    if constexpr (!commit) {
+      if (l < 32) *(f32x2*)(sO + (kFpWaves * GQA + i) * D + 2 * l) = o;
+    } else {
+      sO[(kFpWaves * GQA + i) * D + l] = o[0];
+    }
     if (l == 0) sml[kFpWaves * GQA + i] = f32x2{M, L};
   };
   // merge waves: head i of layer li, the final merge where this workgroup is the last
@@ -622,10 +626,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     if (old == kDoneTarget - 1) {
       if (l == 0)
         __hip_atomic_store(a.done + li * kCntStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (li + 1 < nl)
+      if (li + 1 < nl) {
+        // (agent-coherent stores: the relaxed agent-scope atomic store's form)
+        const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.go);
         for (int x = l; x < (int)gridDim.x; x += 64)
-          __hip_atomic_store(a.go + (size_t)x * kTokGoStride, (uint32_t)(li + 1), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(li + 1), rg, x * (kTokGoStride * 4), 0, kCoherent);
+      }
     }
 #ifdef CIA_TIMELINE
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -657,15 +663,18 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // (the LDS reads done before the next layer's writes)
     bool last = false;
     if (R == 1) {
-      __builtin_amdgcn_raw_buffer_store_b16(f2h(Oa * (1.0f / L)), buf_rsrc(Ly.out), (h * D + d) * 2,
-                                            0, kCoherent);
+      __builtin_amdgcn_raw_buffer_store_b16(f2h(Oa * (1.0f / L)), buf_rsrc(Ly.out), d * 2, h * D * 2,
+                                            kCoherent);
       count_done(li);
     } else {
-      float* row = a.part + ((size_t)(g * kMaxRanges + r) * GQA + i) * kPartRow;
-      __hip_atomic_store(row + 4 + d, Oa, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the row (agent-coherent stores: the relaxed agent-scope atomic
+      // store's form), its base in the scalar offset
+      const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a.part);
+      const int rb = ((g * kMaxRanges + r) * GQA + i) * kPartRow * 4;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, Oa), rp, (4 + d) * 4, rb, kCoherent);
       if (d == 0) {
-        __hip_atomic_store(row, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(row + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, M), rp, 0, rb, kCoherent);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, L), rp, 4, rb, kCoherent);
       }
       stores_acked();
       TL_STAMP(8 * li + 2);
@@ -685,23 +694,27 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     const int i = w - kMergeW0, d = l, h = g * GQA + i;
     uint32_t* tk = a.tick + ((li * NKV + g) * GQA + i) * kCntStride;
     if (d == 0) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.part + (size_t)g * kMaxRanges * kPartF);
+    // (the resource ends at the R partials: reads past them return zero)
+    const __amdgpu_buffer_rsrc_t rs =
+        buf_rsrc(a.part + (size_t)g * kMaxRanges * kPartF, (uint32_t)R * (GQA * kPartRow * 4));
     const __amdgpu_buffer_rsrc_t ro = buf_rsrc(Ly.out);
     // lane p weighs partial p, then lane d sums dim d (the row reads go
     // out together; the weights come from lane p).  NP: 32 partials, or
     // kMaxRanges for the unequal ranges; the terms past R weigh 0.
     auto finish = [&](auto np_tag) {
       constexpr int NP = decltype(np_tag)::value;
-      const int pr = ((l < R ? l : 0) * GQA + i) * kPartRow;
-      const float mp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, pr * 4, 0, kCoherent));
-      const float lp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (pr + 1) * 4, 0, kCoherent));
-      // (one per-lane offset for every row; the row goes in the scalar offset)
-      const int vo = (i * kPartRow + 4 + d) * 4;
+      // (per-lane offsets: lane p's row, dim d; the head and the row of
+      // the dim reads go in the scalar offset)
+      const int ho = i * kPartRow * 4;
+      const int po = l * (GQA * kPartRow * 4);
+      const float mp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, po, ho, kCoherent));
+      const float lp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, po + 4, ho, kCoherent));
+      const int vo = (4 + d) * 4;
       float pv[NP];
 #pragma unroll
       for (int p = 0; p < NP; p++)
         pv[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              rs, vo, (p < R ? p : 0) * (GQA * kPartRow * 4), kCoherent));
+                                              rs, vo, ho + p * (GQA * kPartRow * 4), kCoherent));
       const bool ok = l < R && lp > 0.f;
       const float Mf = wave_max_fast(ok ? mp : -1e30f);
       const float wt = ok ? __builtin_amdgcn_exp2f(mp - Mf) : 0.f;
@@ -711,7 +724,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       for (int p = 0; p < NP; p++)
         Of = __builtin_fmaf(pv[p], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), p)), Of);
       TL_STAMP(8 * li + 4);
-      __builtin_amdgcn_raw_buffer_store_b16(f2h(Of * (1.0f / Lf)), ro, (h * D + d) * 2, 0, kCoherent);
+      __builtin_amdgcn_raw_buffer_store_b16(f2h(Of * (1.0f / Lf)), ro, d * 2, h * D * 2, kCoherent);
     };
     if (R <= 32)
       finish(std::integral_constant<int, 32>{});
@@ -770,15 +783,24 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       merge_part(li);
     }
   } else if (tailw) {
-    for (int li = 0; li < nl; li++) {
-      prep_part(li);
-      b1();
-      TL_STAMP(8 * li);
-      tail_layer(li);
-      b2();
-      TL_STAMP(8 * li + 1);
-      if (w >= kMergeW0) merge_part(li);
-    }
+    // (one loop for the step that commits the group, one for the others:
+    // their registers never meet)
+    auto tail_loop = [&](auto commit_tag) __attribute__((always_inline)) {
+      for (int li = 0; li < nl; li++) {
+        tail_load(li, commit_tag);
+        prep_part(li);
+        b1();
+        TL_STAMP(8 * li);
+        tail_layer(li, commit_tag);
+        b2();
+        TL_STAMP(8 * li + 1);
+        if (w >= kMergeW0) merge_part(li);
+      }
+    };
+    if (commit)
+      tail_loop(T_{});
+    else
+      tail_loop(F_{});
   } else {
     for (int li = 0; li < nl; li++) {
       prep_part(li);
