@@ -708,7 +708,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       const int ho = i * kPartRow * 4;
       const int po = l * (GQA * kPartRow * 4);
       const float mp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, po, ho, kCoherent));
-      const float lp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, po + 4, ho, kCoherent));
+      const float lp = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, po, ho + 4, kCoherent));
       const int vo = (4 + d) * 4;
       float pv[NP];
 #pragma unroll
