@@ -201,7 +201,7 @@ int64_t cia_decode_workspace_bytes(int max_tokens);
 /* cia_attn_decode without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * workspace is a fixed device array inside the library (376 KiB per GPU,
+ * workspace is a fixed device array inside the library (486 KiB per GPU,
  * held until the process ends; it covers every context); the call allocates
  * nothing.  Calls on one GPU share it: calls that overlap on one GPU
  * (several streams or host threads) race.  Same arguments, results and
