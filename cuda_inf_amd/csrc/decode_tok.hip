@@ -19,9 +19,11 @@
 //
 // Across layers.  An FP8 wave's key groups are the same in every layer.
 // After the S^T of its last unit of layer l it sends the first unit of
-// layer l + 1's scales and K into the LDS it has just read, and after that
-// unit's P V its V: the next layer's bytes stream while the rest of layer l
-// (softmax, P V, merges, the wait below) runs.  Layer l + 1's scores start
+// layer l + 1's scales and K into the LDS it has just read, and once the
+// workgroup's part of layer l's merge chain is done (barrier B3) that unit's
+// V: the next layer's bytes stream while the rest of layer l (softmax, P V,
+// merges, the wait below) runs, and the chain's memory operations are not
+// queued behind the V.  Layer l + 1's scores start
 // only when layer l's output is complete, as in the engine, where the next
 // layer's q is computed from it: wave 12 (control) waits until all 32 final
 // merges of layer l have stored their output rows and counted themselves in
@@ -453,8 +455,9 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       if (lin < nl && (kXPre || !lastu)) {
         if (vpre) unit(li, u, lin, un, T_{}, T_{});
         else unit(li, u, lin, un, T_{}, F_{});
-        // the next unit's V, once this unit's P V has read the buffer
-        issue(a.L[lin].vc8, un, vw);
+        // the next unit's V, once this unit's P V has read the buffer (the
+        // next layer's: after B3, issued by the caller)
+        if (!lastu) issue(a.L[lin].vc8, un, vw);
         vpre = true;
       } else {
         if (vpre) unit(li, u, lin, un, F_{}, T_{});
@@ -743,6 +746,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();        // B2: every wave partial of layer li in LDS
   };
+  // B3: the workgroup's part of layer li's merge chain is done (its partials
+  // published and ticketed; where it held a final merge, the output stored
+  // and counted).  Only then do the FP8 waves send the next layer's V: the
+  // compute unit's memory requests are served in order, so the chain's
+  // stores, atomics and loads would otherwise queue behind 64 KiB of V.
+  auto b3 = [&]() { __builtin_amdgcn_s_barrier(); };
   // the merge waves' part of layer li after B2
   auto merge_part = [&](int li) __attribute__((always_inline)) {
     if (merge_publish(li)) merge_finish(li);
@@ -767,6 +776,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       fp8_layer(li);
       b2();
       TL_STAMP(8 * li + 4);
+      b3();
+      if (kXPre && li + 1 < nl) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue(a.L[li + 1].vc8, g0, vw);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (nothing left in flight)
   } else if (w == kCtlW) {
@@ -781,6 +796,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       b2();
       TL_STAMP(8 * li + 1);
       merge_part(li);
+      b3();
     }
   } else if (tailw) {
     // (one loop for the step that commits the group, one for the others:
@@ -795,6 +811,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
         b2();
         TL_STAMP(8 * li + 1);
         if (w >= kMergeW0) merge_part(li);
+        b3();
       }
     };
     if (commit)
@@ -809,6 +826,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       b2();
       TL_STAMP(8 * li + 1);
       merge_part(li);
+      b3();
     }
   }
 #ifdef CIA_TIMELINE
