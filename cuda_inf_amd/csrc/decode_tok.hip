@@ -736,8 +736,8 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     count_done(li);
   };
   // Each role runs its own loop over the layers (so that no role's registers
-  // stay live through another's code); every wave passes B1 and B2 of each
-  // layer in order.
+  // stay live through another's code); every wave passes B1, B2 and B3 of
+  // each layer in order (and B0 with the producers).
   auto b1 = [&]() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS stores done (DMAs still in flight)
     __builtin_amdgcn_s_barrier();        // B1: layer li's q rows and fresh token in LDS
@@ -838,8 +838,9 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
 
 using namespace cia;
 
-// kXPre: the next layer's first unit streams while a layer merges (measured
-// 70.0 against 71.9 us/token without, 32 768 keys x 6 layers)
+// kXPre: the next layer's first unit streams while a layer merges (its K
+// after the last S^T, its V after B3; measured 70.0 against 71.9 us/token
+// without, 32 768 keys x 6 layers, when the V went out after P V)
 constexpr bool kTokXPre = true;
 
 // The layers of one decode step in one launch when they qualify: every
