@@ -242,8 +242,6 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
 #pragma unroll
     for (int mu = 0; mu < 4; mu++) vrd[mu] = base + 256 * ((c + mu) & 3);
   }
-  const int koff = 4 * (n >> 2) + c;  // key of output element v: 16 v + koff of the tile
-  (void)koff;
   f16x8 qop[8];
   float mx = -1e30f, lsum = 0.f;
   f32x4 O[4];
