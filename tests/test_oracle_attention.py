@@ -249,9 +249,10 @@ def test_decode_mt_equals_single_thread(orc):
 
 
 def test_fused_mt_equals_single_thread(orc):
-    """The threaded head-range form of attention_fused (the checker of the
-    4096-token prefill's every row) gives the single-threaded oracle's bits
-    for the heads it covers and leaves the others zero."""
+    """The threaded head-range form of attention_fused (the reference that
+    the 4096-token prefill's every row is compared with) gives the
+    single-threaded oracle's bits for the heads it covers and leaves the
+    others zero."""
     rng = np.random.default_rng(23)
     S, past = 90, 40
     c, _, _ = make_cache(orc, rng, past + S)
