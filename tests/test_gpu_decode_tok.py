@@ -193,3 +193,39 @@ def test_one_launch_6_layers_64_steps_vs_oracle(orc, cia, dev):
         nt = n0 + steps - c
         assert np.array_equal(_u16(L.ktail).reshape(64, -1)[:nt], refs[l].ktail.reshape(64, -1)[:nt])
         assert np.array_equal(_u16(L.vtail).reshape(64, -1)[:nt], refs[l].vtail.reshape(64, -1)[:nt])
+
+
+@pytest.mark.parametrize("nL", [1, 8, 9])
+def test_layer_counts_and_chunks(orc, cia, dev, nL):
+    """One layer in the one-launch kernel, the most layers one launch takes
+    (8), and 9 layers (a launch of 8, then one of 1): the cache bytes and
+    the outputs bit-identical to one launch per layer over 6 steps that
+    cross the commit of group 64 (4155 keys: one unit per FP8 wave), and
+    the fault word 0."""
+    from cuda_inf_amd import _lib
+    print(f"layer counts: {nL} layers", flush=True)
+    n0, steps = 4155, 6
+    maxT = n0 + steps + 64
+    g = np.random.default_rng(900 + nL)
+    q = (g.standard_normal((steps, nL, 32, 64)) * 2).astype(np.float16)
+    k = (g.standard_normal((steps, nL, 8, 64)) * 2).astype(np.float16)
+    v = g.standard_normal((steps, nL, 8, 64)).astype(np.float16)
+    qd, kd, vd = _t16(q, dev), _t16(k, dev), _t16(v, dev)
+    runs = []
+    for per in (1, 0):
+        layers = _layers(dev, n0, nL, 700, maxT)
+        arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+        out = torch.zeros((steps, nL, 32, 64), dtype=torch.float16, device=dev)
+        _lib.call("cia_decode_loop_ex", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                  out.data_ptr(), n0, steps, 0.125, per, None,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        runs.append((layers, arr, out))
+    (la, aa, oa), (lb, ab, ob) = runs
+    assert _fault(lb[0]) == 0, "a bounded wait gave up"
+    for l in range(nL):
+        assert aa[l].committed == ab[l].committed == (n0 + steps) // 64 * 64
+        for name in NAMES:
+            x, y = getattr(la[l], name), getattr(lb[l], name)
+            assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), (l, name)
+    assert np.array_equal(_u16(oa), _u16(ob)), "outputs not bit-identical"
