@@ -195,16 +195,18 @@ def test_one_launch_6_layers_64_steps_vs_oracle(orc, cia, dev):
         assert np.array_equal(_u16(L.vtail).reshape(64, -1)[:nt], refs[l].vtail.reshape(64, -1)[:nt])
 
 
-@pytest.mark.parametrize("nL", [1, 8, 9])
-def test_layer_counts_and_chunks(orc, cia, dev, nL):
+@pytest.mark.parametrize("nL,n0", [(1, 4155), (8, 4155), (9, 4155), (3, 637), (3, 1535)])
+def test_layer_counts_and_chunks(orc, cia, dev, nL, n0):
     """One layer in the one-launch kernel, the most layers one launch takes
-    (8), and 9 layers (a launch of 8, then one of 1): the cache bytes and
-    the outputs bit-identical to one launch per layer over 6 steps that
-    cross the commit of group 64 (4155 keys: one unit per FP8 wave), and
+    (8), and 9 layers (a launch of 8, then one of 1) at 4155 keys; and the
+    small contexts with one workgroup per kv head (637 keys: the output
+    stored without a cross-workgroup merge) and two (1535 keys).  The cache
+    bytes and the outputs bit-identical to one launch per layer over 6
+    steps that cross a group commit (one unit per FP8 wave everywhere), and
     the fault word 0."""
     from cuda_inf_amd import _lib
-    print(f"layer counts: {nL} layers", flush=True)
-    n0, steps = 4155, 6
+    print(f"layer counts: {nL} layers at {n0} keys", flush=True)
+    steps = 6
     maxT = n0 + steps + 64
     g = np.random.default_rng(900 + nL)
     q = (g.standard_normal((steps, nL, 32, 64)) * 2).astype(np.float16)
