@@ -86,6 +86,13 @@ __device__ __forceinline__ u32x2 ds_read_tr8_at(const uint8_t* p) {
 __device__ __forceinline__ void lds_wait4(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
+// the same, leaving the kN LDS reads issued after these four in flight (LDS
+// reads complete in order; another pending lgkm operation only makes the
+// wait longer)
+template <int kN>
+__device__ __forceinline__ void lds_wait4_but(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(kN));
+}
 
 // Publishing a partial to the other workgroups: its agent-coherent stores
 // (relaxed agent-scope atomics) are acknowledged -- vmcnt(0): a store's
@@ -100,6 +107,19 @@ __device__ __forceinline__ void stores_acked() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   asm volatile("" ::: "memory");
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// A polled word read on the scalar path: one s_load_dword with glc (a miss
+// in the scalar cache, read from L2), then its wait.  The vector memory
+// requests of a compute unit are served in order, so a vector poll waits
+// behind the DMAs the workgroup's other waves have just sent; this load
+// does not.  The word is written by agent-coherent stores from any XCD;
+// the caller's wait is bounded and records a fault if the value never
+// arrives.  p must be uniform and 4-byte aligned.
+__device__ __forceinline__ uint32_t scalar_poll(const uint32_t* p) {
+  uint32_t v;
+  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p) {
