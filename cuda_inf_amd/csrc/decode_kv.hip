@@ -538,21 +538,10 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       // ---- O = O corr + (P sv) V
       if constexpr (kMore) __builtin_amdgcn_s_waitcnt(0x0F7A);  // vmcnt(10): next scales + K in flight
       else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
-      const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       f32x4 T[4];
 #pragma unroll
       for (int d = 0; d < 4; d++) T[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mu = 0; mu < 4; mu++) {
-        const f16x8 A = ((n >> 2) == ((c + mu) & 3)) ? P : zero8;
-        u32x2 raw0 = ds_read_tr8(vw + vrd[mu], 0), raw1 = ds_read_tr8(vw + vrd[mu], 16);
-        u32x2 raw2 = ds_read_tr8(vw + vrd[mu], 32), raw3 = ds_read_tr8(vw + vrd[mu], 48);
-        lds_wait4(raw0, raw1, raw2, raw3);
-        T[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw0[0], raw0[1]), T[0], 0, 0, 0);
-        T[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw1[0], raw1[1]), T[1], 0, 0, 0);
-        T[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw2[0], raw2[1]), T[2], 0, 0, 0);
-        T[3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(raw3[0], raw3[1]), T[3], 0, 0, 0);
-      }
+      unit_pv(T, P, vw, vrd, n, c);
       if constexpr (kMore) {
         // this unit's V fully read: the caller sends the next unit's V
         __builtin_amdgcn_s_waitcnt(0xC07F);

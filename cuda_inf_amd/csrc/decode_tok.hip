@@ -330,38 +330,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     if constexpr (kMore) __builtin_amdgcn_s_waitcnt(0x0F7A);  // vmcnt(10): next scales + K in flight
     else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
     if (u == g0) TL_STAMP(8 * li + 2);
-    const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     f32x4 T[4];
 #pragma unroll
     for (int d = 0; d < 4; d++) T[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // the V^T reads of two products in flight at once, each product as soon
-    // as its four reads are in (54.9-55.0 -> 54.7-54.9 us per token against
-    // one product's reads at a time, A/B on one box)
-    u32x2 rw[4][4];
-    auto pv_read = [&](int mu) __attribute__((always_inline)) {
-      rw[mu][0] = ds_read_tr8(vw + vrd[mu], 0);
-      rw[mu][1] = ds_read_tr8(vw + vrd[mu], 16);
-      rw[mu][2] = ds_read_tr8(vw + vrd[mu], 32);
-      rw[mu][3] = ds_read_tr8(vw + vrd[mu], 48);
-    };
-    auto pv_mma = [&](int mu) __attribute__((always_inline)) {
-      const f16x8 A = ((n >> 2) == ((c + mu) & 3)) ? P : zero8;
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        T[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(rw[mu][j][0], rw[mu][j][1]), T[j], 0, 0, 0);
-    };
-    pv_read(0);
-    pv_read(1);
-    lds_wait4_but<4>(rw[0][0], rw[0][1], rw[0][2], rw[0][3]);
-    pv_mma(0);
-    pv_read(2);
-    lds_wait4_but<4>(rw[1][0], rw[1][1], rw[1][2], rw[1][3]);
-    pv_mma(1);
-    pv_read(3);
-    lds_wait4_but<4>(rw[2][0], rw[2][1], rw[2][2], rw[2][3]);
-    pv_mma(2);
-    lds_wait4(rw[3][0], rw[3][1], rw[3][2], rw[3][3]);
-    pv_mma(3);
+    // (the V^T reads of two products in flight: 54.9-55.0 -> 54.7-54.9 us
+    // per token against one product's reads at a time, A/B on one box)
+    unit_pv(T, P, vw, vrd, n, c);
     if constexpr (kMore) {
       // this unit's V fully read: the caller sends the next unit's V
       __builtin_amdgcn_s_waitcnt(0xC07F);

@@ -94,6 +94,41 @@ __device__ __forceinline__ void lds_wait4_but(u32x2& a, u32x2& b, u32x2& c, u32x
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(kN));
 }
 
+// P V of one unit into T (zeroed by the caller): in product mu the k-group
+// c of V^T holds key block (c + mu) & 3, so A = P on the lanes whose block
+// that is and zero elsewhere; V^T comes from LDS at vw + vrd[mu] through
+// the transposing read.  The reads of two products are in flight at once,
+// each product issued as soon as its four reads are in.
+__device__ __forceinline__ void unit_pv(f32x4 (&T)[4], const f16x8& P, const uint8_t* vw, const int (&vrd)[4],
+                                        int n, int c) {
+  const f16x8 zero8 = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  u32x2 rw[4][4];
+  auto rd = [&](int mu) __attribute__((always_inline)) {
+    rw[mu][0] = ds_read_tr8(vw + vrd[mu], 0);
+    rw[mu][1] = ds_read_tr8(vw + vrd[mu], 16);
+    rw[mu][2] = ds_read_tr8(vw + vrd[mu], 32);
+    rw[mu][3] = ds_read_tr8(vw + vrd[mu], 48);
+  };
+  auto mma = [&](int mu) __attribute__((always_inline)) {
+    const f16x8 A = ((n >> 2) == ((c + mu) & 3)) ? P : zero8;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      T[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, cvt8(rw[mu][j][0], rw[mu][j][1]), T[j], 0, 0, 0);
+  };
+  rd(0);
+  rd(1);
+  lds_wait4_but<4>(rw[0][0], rw[0][1], rw[0][2], rw[0][3]);
+  mma(0);
+  rd(2);
+  lds_wait4_but<4>(rw[1][0], rw[1][1], rw[1][2], rw[1][3]);
+  mma(1);
+  rd(3);
+  lds_wait4_but<4>(rw[2][0], rw[2][1], rw[2][2], rw[2][3]);
+  mma(2);
+  lds_wait4(rw[3][0], rw[3][1], rw[3][2], rw[3][3]);
+  mma(3);
+}
+
 // Publishing a partial to the other workgroups: its agent-coherent stores
 // (relaxed agent-scope atomics) are acknowledged -- vmcnt(0): a store's
 // count drops when the L2 of this XCD has written it through -- before the
