@@ -153,6 +153,23 @@ __device__ __forceinline__ float col4_sum(float v) {
   r = swap32(v);
   return r[0] + r[1];
 }
+// col4_sum of four registers at once: lane l of the result holds register
+// (l >> 4)'s sum for column l & 15 (a, b, c, d for lane blocks 0..3).  The
+// same additions in the same order as col4_sum, with 3 swaps and 3 adds
+// where four col4_sum take 8 of each.
+__device__ __forceinline__ float col4_sum4(float a, float b, float c, float d) {
+  // permlane16_swap(x, y): x gets rows (x0, y0, x2, y2), y rows (x1, y1, x3, y3)
+  const auto ab = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                   false, false);
+  const auto cd = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d),
+                                                   false, false);
+  const float x = __builtin_bit_cast(float, (uint32_t)ab[0]) + __builtin_bit_cast(float, (uint32_t)ab[1]);
+  const float y = __builtin_bit_cast(float, (uint32_t)cd[0]) + __builtin_bit_cast(float, (uint32_t)cd[1]);
+  // permlane32_swap(x, y): x gets halves (x_lo, y_lo), y (x_hi, y_hi)
+  const auto xy = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y),
+                                                   false, false);
+  return __builtin_bit_cast(float, (uint32_t)xy[0]) + __builtin_bit_cast(float, (uint32_t)xy[1]);
+}
 // max over the wave (exact in any order)
 __device__ __forceinline__ float wave_max_fast(float v) {
   v = __builtin_fmaxf(v, row_ror<8>(v));

@@ -684,18 +684,11 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
     }
     if constexpr (!kSplit) {
-      // ---- the four key blocks of each (head, dim) summed; lanes 0..15 hold
-      // O[head v][16 delta + n]
+      // ---- the four key blocks of each (head, dim) summed: lane l holds
+      // head l >> 4, dim 16 delta + (l & 15)
 #pragma unroll
       for (int d = 0; d < 4; d++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) O[d][v] = col4_sum(O[d][v]);
-      if (l < 16) {
-#pragma unroll
-        for (int d = 0; d < 4; d++)
-#pragma unroll
-          for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = O[d][v];
-      }
+        sO[(w * GQA + (l >> 4)) * D + 16 * d + (l & 15)] = col4_sum4(O[d][0], O[d][1], O[d][2], O[d][3]);
       if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
     }
   } else if constexpr (kSplit) {

@@ -459,19 +459,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       if (lastu) break;
     }
     TL_STAMP(8 * li + 3);
-    // the four key blocks of each (head, dim) summed; lanes 0..15 hold
-    // O[head v][16 delta + n]
+    // the four key blocks of each (head, dim) summed: lane l holds head
+    // l >> 4, dim 16 delta + (l & 15)
     const int pw = xw ? kFpWaves : w;
 #pragma unroll
     for (int d = 0; d < 4; d++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) O[d][v] = col4_sum(O[d][v]);
-    if (l < 16) {
-#pragma unroll
-      for (int d = 0; d < 4; d++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) sO[(pw * GQA + v) * D + 16 * d + l] = O[d][v];
-    }
+      sO[(pw * GQA + (l >> 4)) * D + 16 * d + (l & 15)] = col4_sum4(O[d][0], O[d][1], O[d][2], O[d][3]);
     if (l < GQA) sml[pw * GQA + l] = f32x2{mx, lsum};
   };
   // tail waves (range 0): layer li's fp16 tail, fresh token and commit.
