@@ -139,6 +139,23 @@ def main():
             st_ = rel(tl[wg, w, b:b + 8], t0)
             st_[tl[wg, w, b:b + 8] == 0] = np.nan
             print(f"    wave {w:2d}: " + " ".join(f"{x:7.2f}" for x in st_))
+    # how often the last workgroup to B2 of layer li held a final merge of
+    # layer li - 1 (its merge waves' stamp 4 set), and how much later the
+    # final mergers' latest B2 is than the others' (medians over tokens)
+    hits, tot, gap = 0, 0, []
+    for smp in samples:
+        tl = smp[:nwg]
+        t0 = int(tl[:, :8, 63].min())
+        for li in range(1, nL):
+            b2 = rel(tl[:, :8, 8 * li + 4], t0).max(axis=1)
+            fm = (tl[:, 9:13, 8 * (li - 1) + 4] != 0).any(axis=1)
+            hits += int(fm[int(np.argmax(b2))])
+            tot += 1
+            if fm.any() and (~fm).any():
+                gap.append(float(b2[fm].max() - b2[~fm].max()))
+    if gap:
+        print(f"  last workgroup to B2 held a final merge of the layer before in {hits}/{tot} layers; "
+              f"final mergers' latest B2 - the others' latest: {np.median(gap):.2f} us")
     keys = list(rows[0].keys())
     for key in keys:
         med = st.median(float(np.median(r[key])) for r in rows)
