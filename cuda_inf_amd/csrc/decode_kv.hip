@@ -574,45 +574,33 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
     } else {
       // a finished split (or share): its (m, l, o) per head, then a fresh state
       auto flush = [&](int sp) {
-        f32x4 Oc[4];
+        // the four key blocks summed: lane l holds head hl = l >> 4, dim
+        // 16 d + dl of Oc[d]
+        const int hl = l >> 4, dl = l & 15;
+        float Oc[4];
 #pragma unroll
-        for (int d = 0; d < 4; d++)
-#pragma unroll
-          for (int v = 0; v < 4; v++) Oc[d][v] = col4_sum(O[d][v]);
+        for (int d = 0; d < 4; d++) Oc[d] = col4_sum4(O[d][0], O[d][1], O[d][2], O[d][3]);
         if (kRange && sp > s0) {
           // range mode, the wave's second split (always its last): its
           // partial into the wave's own K tile, free once the stream is done
           float* x = (float*)(lds + kLdsK + (w & 7) * kHalfB);
-          if (l < 16) {
 #pragma unroll
-            for (int d = 0; d < 4; d++)
-#pragma unroll
-              for (int v = 0; v < 4; v++) x[v * kPartRow + 4 + 16 * d + l] = Oc[d][v];
-          }
+          for (int d = 0; d < 4; d++) x[hl * kPartRow + 4 + 16 * d + dl] = Oc[d];
           if (l < GQA) {
             x[l * kPartRow] = mx;
             x[l * kPartRow + 1] = lsum;
           }
           f1 = true;
         } else if (ns >= kFpWaves) {  // (then every split has one wave; else all go through the merge)
-          if (l < 16) {
 #pragma unroll
-            for (int d = 0; d < 4; d++)
-#pragma unroll
-              for (int v = 0; v < 4; v++)
-                a.po[((size_t)(g * GQA + v) * a.nsplit + sp) * D + 16 * d + l] = Oc[d][v];
-          }
+          for (int d = 0; d < 4; d++) a.po[((size_t)(g * GQA + hl) * a.nsplit + sp) * D + 16 * d + dl] = Oc[d];
           if (l < GQA) {
             a.pm[(g * GQA + l) * a.nsplit + sp] = lsum > 0.f ? mx * kLn2 : -1e30f;
             a.pl[(g * GQA + l) * a.nsplit + sp] = lsum;
           }
         } else {
-          if (l < 16) {
 #pragma unroll
-            for (int d = 0; d < 4; d++)
-#pragma unroll
-              for (int v = 0; v < 4; v++) sO[(w * GQA + v) * D + 16 * d + l] = Oc[d][v];
-          }
+          for (int d = 0; d < 4; d++) sO[(w * GQA + hl) * D + 16 * d + dl] = Oc[d];
           if (l < GQA) sml[w * GQA + l] = f32x2{mx, lsum};
         }
         mx = -1e30f;
