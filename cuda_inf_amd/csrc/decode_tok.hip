@@ -82,7 +82,8 @@ static_assert(tBytes <= 160 * 1024, "LDS");
 // landed, 2 its V landed, 3 units done, 4 partials in LDS; merge waves:
 // 0 opened, 1 partials in LDS, 2 own partial acknowledged, 3 ticket,
 // 4 final rows fetched, 5 output counted; control: 6 wait begun, 7 q rows
-// loaded); lane 63: the wave's start.
+// loaded; tail waves of range 0: 6 tail rows landed, 7 tail done); lane 63:
+// the wave's start.
 #ifdef CIA_TIMELINE
 constexpr int kTlMaxWg = 8 * kMaxRanges;
 __device__ uint32_t tl_buf[kTlMaxWg * kTokWaves * 64];
@@ -483,6 +484,10 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     constexpr bool commit = decltype(commit_tag)::value;
     const TokLayer& Ly = a.L[li];
     const int i = w - kFpWaves;  // query head 4g + i
+#ifdef CIA_TIMELINE
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // (the rows landed: the stamp after them)
+    TL_STAMP(8 * li + 6);
+#endif
     if (i == 0) {
       // the fresh token into its tail row (engine.cu:190-198)
       Ly.ktail[((size_t)(tt - 1) * NKV + g) * D + l] = skn[l];
@@ -594,6 +599,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       sO[(kFpWaves * GQA + i) * D + l] = o[0];
     }
     if (l == 0) sml[kFpWaves * GQA + i] = f32x2{M, L};
+    TL_STAMP(8 * li + 7);
   };
   // merge waves: head i of layer li, the final merge where this workgroup is the last
   // merge waves: head i of layer li.  merge_publish: the workgroup's partial

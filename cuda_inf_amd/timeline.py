@@ -10,8 +10,9 @@ tokens of each event's time since the launch's first wave started.
 Printed per layer: the FP8 waves' "opened" (B1 passed), first unit's K
 landed, V landed, units done and partials-in-LDS (B2); the merge waves'
 partial acknowledged, ticket, final rows fetched (last arrivers) and output
-counted; the control wave's wait begun and q loaded.  Each as median / max
-over waves (median over tokens), in microseconds.
+counted; the control wave's wait begun and q loaded; range 0's tail waves'
+rows landed and tail done.  Each as median / max over waves (median over
+tokens), in microseconds.
 """
 from __future__ import annotations
 
@@ -123,6 +124,11 @@ def main():
             if li > 0:
                 res[(li, "control: wait begun")] = ctl[:, 0]
             res[(li, "control: q loaded")] = ctl[:, 1]
+            # range 0's tail waves (8-11): rows landed, tail done
+            r0 = [x for x in range(nwg) if (x & 7) < 4 and (x >> 3) < 2] if R > 1 else list(range(nwg))
+            tw = rel(tl[r0][:, 8:12, b + 6:b + 8], t0)
+            res[(li, "tail: rows landed")] = tw[:, :, 0]
+            res[(li, "tail: done")] = tw[:, :, 1]
         rows.append(res)
         buf[:] = 0
     # the workgroup that reached "partials in LDS" last in each layer of
