@@ -79,7 +79,8 @@ static_assert(tBytes <= 160 * 1024, "LDS");
 // waits are unchanged), and stores them once at its end into
 // tl_buf[workgroup][wave][64]; cia_timeline_read copies them out.  Stamp k
 // of layer li is lane 8 li + k (FP8 waves: 0 opened, 1 first unit's K
-// landed, 2 its V landed, 3 units done, 4 partials in LDS; merge waves:
+// landed, 2 its V landed, 3 units done, 4 partials in LDS, 5 the next
+// layer's K sent, 6 the next layer's V sent; merge waves:
 // 0 opened, 1 partials in LDS, 2 own partial acknowledged, 3 ticket,
 // 4 final rows fetched, 5 output counted; control: 6 wait begun, 7 q rows
 // loaded; tail waves of range 0: 6 tail rows landed, 7 tail done); lane 63:
@@ -293,6 +294,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       issue_scales(lin, un, sw + (slot ^ 1) * 2 * kScaleB);
       issue(a.L[lin].kc8, un, kw);
       __builtin_amdgcn_sched_barrier(0);
+      if (lin != li) TL_STAMP(8 * li + 5);
     }
     // ---- online softmax over the unit's 128 keys (4 per lane and tile)
     float rmx = -1e30f;
@@ -771,6 +773,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         issue(a.L[li + 1].vc8, g0, vw);
         __builtin_amdgcn_sched_barrier(0);
+        TL_STAMP(8 * li + 6);
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (nothing left in flight)

@@ -8,7 +8,8 @@ tokens of each event's time since the launch's first wave started.
     python -m cuda_inf_amd.timeline [--ctx 32768] [--layers 6] [--tokens 32]
 
 Printed per layer: the FP8 waves' "opened" (B1 passed), first unit's K
-landed, V landed, units done and partials-in-LDS (B2); the merge waves'
+landed, V landed, units done, partials-in-LDS (B2) and the next layer's K
+and V sent; the merge waves'
 partial acknowledged, ticket, final rows fetched (last arrivers) and output
 counted; the control wave's wait begun and q loaded; range 0's tail waves'
 rows landed and tail done.  Each as median / max over waves (median over
@@ -116,6 +117,10 @@ def main():
             res[(li, "fp8 V landed")] = fp8[:, :, 2]
             res[(li, "fp8 units done")] = fp8[:, :, 3]
             res[(li, "partials in LDS")] = fp8[:, :, 4]
+            if li + 1 < nL:
+                nx = rel(tl[:, :8, b + 5:b + 7], t0)
+                res[(li, "fp8: next K sent")] = nx[:, :, 0]
+                res[(li, "fp8: next V sent")] = nx[:, :, 1]
             res[(li, "merge: partial acked")] = mw[:, :, 2]
             res[(li, "merge: ticket")] = mw[:, :, 3]
             last = tl[:, 9:13, b + 4] != 0
