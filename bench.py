@@ -9,10 +9,14 @@ fresh K/V through the tail (and the FP8 commit when a group fills) and run
 the attention.  Synthetic seeded inputs (N(0,1); K/V with 1% outliers x20;
 Q with QK-RMSNorm + RoPE), resident in HBM before timing starts.
 
+The decode loop launches k_decode_tok once per run of consecutive tokens
+(up to the token that fills a group); one launch per token and one launch
+per layer are timed beside it on the same tokens.
+
 Printed: one JSON line with µs/token (warm: consecutive tokens; cold: the
-256 MB Infinity Cache flushed before every token), the decode kernel's
-roofline against 8 TB/s, a causal-prefill leg (4096 tokens), and the CPU
-oracle timed on this host as a baseline.
+256 MB Infinity Cache flushed before every token, one launch per token),
+the decode kernel's roofline against 8 TB/s, a causal-prefill leg (4096
+tokens), and the CPU oracle timed on this host as a baseline.
 
     python bench.py [--steps 256] [--warmup 10] [--ctx 32768] [--layers 6]
 """
@@ -52,9 +56,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", type=float, default=None,
-                    help="HBM bytes per decode launch measured with rocprofv3 --pmc "
-                         "(FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), reported as "
-                         "roofline.traffic")
+                    help="HBM bytes per decode token measured with rocprofv3 --pmc "
+                         "(FETCH_SIZE + WRITE_SIZE, copy-kernel scaled); roofline.traffic "
+                         "is this times the timed launches' tokens per launch")
     ap.add_argument("--long-ctx", type=int, default=131072,
                     help="long-context decode leg: context tokens (0 = skip)")
     ap.add_argument("--long-steps", type=int, default=8)
@@ -91,7 +95,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     nL, ctx, K, W = a.layers, a.ctx, a.steps, a.warmup
-    total_steps = W + 3 * K + 2 + a.cold_steps + a.prep_steps + a.block_steps + a.split_steps
+    total_steps = W + 4 * K + 4 + a.cold_steps + a.prep_steps + a.block_steps + a.split_steps
     maxT = ctx + total_steps + 64
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)  # noqa: E731
     log(f"device {torch.cuda.get_device_name(dev)}; ctx {ctx}, layers {nL}, steps {K}")
@@ -133,16 +137,27 @@ def main():
     qrow, krow = nL * NH * D, nL * NKV * D
     cur = {"step": 0}
 
-    def run(steps, events=None, per=0):
-        """steps decode tokens through cia_decode_loop_ex: per = 0 runs the
+    def run(steps, events=None, per=0, tpl=0):
+        """steps decode tokens through cia_decode_loop_runs: per = 0 runs the
         layers of a token in one launch (k_decode_tok), 1 one launch per
-        layer (k_decode)"""
+        layer (k_decode); tpl = 0 runs consecutive tokens in one launch up
+        to each group fill, 1 one launch per token"""
         s0 = cur["step"]
-        call("cia_decode_loop_ex", arr, nL, q.data_ptr() + s0 * qrow * 2,
+        call("cia_decode_loop_runs", arr, nL, q.data_ptr() + s0 * qrow * 2,
              kk.data_ptr() + s0 * krow * 2, vv.data_ptr() + s0 * krow * 2,
-             out.data_ptr() + s0 * qrow * 2, ctx + s0, steps, 0.125, per, events,
+             out.data_ptr() + s0 * qrow * 2, ctx + s0, steps, 0.125, per, tpl, events,
              stream.cuda_stream)
         cur["step"] += steps
+
+    def launches_of_steps(s0, steps):
+        """k_decode_tok launches of the decode loop over steps s0.. : runs
+        of tokens, each ending at the token that fills a group (the tail
+        holds (ctx + s) % 64 tokens before step s)"""
+        n, i = 0, 0
+        while i < steps:
+            i += min(steps - i, 64 - (ctx + s0 + i) % 64)
+            n += 1
+        return n
 
     def bytes_of_steps(s0, steps):
         tot = 0
@@ -167,19 +182,22 @@ def main():
     timed_bytes = bytes_of_steps(s_timed, K)
     log(f"warm: {us_tok:.2f} us/token, effective {timed_bytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s")
 
-    # The decode launch (k_decode_tok, one per token for all nL layers: per
-    # layer the FP8 stream, the tail, the fresh token's write and the merge,
-    # layer l + 1 scored after layer l's output is stored) is the dominant
-    # work: its average duration is the timed region's span over its K
-    # launches (events bracket the region on the kernels' own stream; 1 step
-    # in 64 also carries every layer's FP8 commit).
-    dec_us = warm_ms * 1e3 / K
-    dec_bytes = timed_bytes / K
+    # The decode launch (k_decode_tok: a run of consecutive tokens, all nL
+    # layers of each; per layer the FP8 stream, the tail, the fresh token's
+    # write and the merge, each layer scored after the one before it has
+    # stored its output) is the dominant work.  The decode loop ends a run
+    # at the token that fills a group (its FP8 commit), so the timed region's
+    # launches are its segments between group fills; their average duration
+    # is the region's span over their count (events bracket the region on
+    # the kernels' own stream).
+    n_launch = launches_of_steps(s_timed, K) if a.nsplit == 0 else K
+    dec_us = warm_ms * 1e3 / n_launch
+    dec_bytes = timed_bytes / n_launch
     achieved = dec_bytes / (dec_us * 1e-6) / 1e9
 
-    # ---- the same launches one by one: HIP events recorded by the decode
-    # loop right before and after each token's launch (each event adds its
-    # own marker overhead)
+    # ---- one token per launch: HIP events recorded by the decode loop right
+    # before and after each token's launch (with events the loop launches
+    # token by token; each event adds its own marker overhead)
     nev = 3 * K * nL
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(nev)]
     for e in evs:  # the hipEvent_t handles exist once recorded
@@ -190,8 +208,24 @@ def main():
     torch.cuda.synchronize()
     one = sorted(evs[3 * nL * r].elapsed_time(evs[3 * nL * r + 1]) * 1e3 for r in range(K))
     ev_us = one[len(one) // 2]
-    log(f"decode launch: {dec_us:.2f} us per token ({nL} layers), {dec_bytes / 1e6:.2f} MB, "
-        f"{achieved:.0f} GB/s; event-bracketed median {ev_us:.2f} us")
+    log(f"decode launches: {n_launch} for {K} tokens, {dec_us:.2f} us and {dec_bytes / 1e6:.2f} MB "
+        f"each, {achieved:.0f} GB/s; one token per launch (event-bracketed): median {ev_us:.2f} us")
+
+    # ---- the same tokens with one launch per token (k_decode_tok, all
+    # layers of the token; back to back, no events)
+    run(2, tpl=1)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(K, tpl=1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ot_ms = e0.elapsed_time(e1)
+    ot_bytes = bytes_of_steps(cur["step"] - K, K)
+    one_token = {"us_per_token": round(ot_ms * 1e3 / K, 3),
+                 "gbps": round(ot_bytes / (ot_ms * 1e-3) / 1e9, 1),
+                 "kernel": f"k_decode_tok (one launch per token: {nL} layers)"}
+    log(f"one launch per token: {one_token['us_per_token']:.2f} us/token "
+        f"({one_token['gbps']:.0f} GB/s)")
 
     # ---- the same tokens with one launch per layer (k_decode; the
     # reference's per-layer launch structure)
@@ -232,7 +266,7 @@ def main():
     floor_bytes = 2 * arr[0].committed * NKV * D
     floor_gbps = floor_bytes / (floor_us * 1e-6) / 1e9
     log(f"plain read of the same bytes: {floor_us:.2f} us per layer, {floor_gbps:.0f} GB/s "
-        f"({dec_us / (nL * floor_us):.2f}x the decode's time)")
+        f"({us_tok / (nL * floor_us):.2f}x the decode's time per token)")
 
     # ---- cold: evict the KV from the 256 MB Infinity Cache before every token
     # by reading 1 GiB of other data (a read leaves no dirty lines behind)
@@ -556,7 +590,11 @@ def main():
     if h2o is not None:
         h2o["cpu_baseline"] = cpu_h2o
 
+    # HBM bytes per launch: per token from the committed counters, times
+    # the timed launches' tokens
     traffic = a.traffic if a.traffic is not None else measured_traffic(ctx, nL)
+    if traffic is not None:
+        traffic = int(round(traffic * K / n_launch))
     res = {
         "metric": "decode-attn µs/token + HBM GB/s (% of 8 TB/s) at 32k ctx; prefill MFMA util",
         "value": round(us_tok, 3),
@@ -572,8 +610,9 @@ def main():
         "data": "synthetic: seeded N(0,1), K/V 1% outliers x20, Q QK-RMSNorm+RoPE",
         "config": {"workload": f"flash-decoding, ctx {ctx}, {nL} attention layers/token, batch 1, "
                                f"32Q/8KV heads, d64, FP8 E4M3 group-64 KV + fp16 tail",
-                   "context": ctx, "layers": nL, "decode": "matrix-core, one launch per token "
-                   "(all layers; layer l+1 scored after layer l's output)"
+                   "context": ctx, "layers": nL, "decode": "matrix-core, one launch per run of "
+                   "tokens up to each group fill (all layers; each layer scored after the "
+                   "one before it has stored its output)"
                    if a.nsplit == 0 else f"split+combine nsplit={a.nsplit}"},
         "effective_gbps_warm": round(timed_bytes / (warm_ms * 1e-3) / 1e9, 1),
         "cold_us_per_token": round(cold_us, 3) if cold_us else None,
@@ -582,10 +621,12 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "traffic_source": TRAFFIC_FILE + " (not this run)" if traffic else None,
-                     "kernel": f"k_decode_tok (one launch per token: {nL} layers)",
+                     "kernel": f"k_decode_tok (one launch per run of tokens: {nL} layers each)",
+                     "launches": n_launch,
+                     "tokens_per_launch": round(K / n_launch, 2),
                      "algo_bytes_per_launch": int(dec_bytes),
                      "avg_launch_us": round(dec_us, 3),
-                     "event_bracketed_median_us": round(ev_us, 3),
+                     "one_token_launch_median_us": round(ev_us, 3),
                      "measured_ceiling": {
                          "kernel": "k_stream_read (plain read of the same FP8 K+V, one "
                                    "launch per layer)",
@@ -593,6 +634,7 @@ def main():
                          "frac": round(achieved / floor_gbps, 4),
                          "cold_us_per_token": round(floor_cold_us, 3) if floor_cold_us else None,
                          "cold_frac": round(floor_cold_us / cold_us, 4) if floor_cold_us else None}},
+        "one_token_launches": one_token,
         "per_layer_launches": per_layer,
         "prefill": prefill,
         "split16": split16,
@@ -824,7 +866,7 @@ def h2o_leg(steps, dev, stream, log, C=2048, W=256, P=1024):
 
 
 def measured_traffic(ctx: int, nL: int):
-    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary
+    """HBM bytes per decode token from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) when it was taken on this
     workload; None otherwise."""
     p = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
@@ -835,7 +877,7 @@ def measured_traffic(ctx: int, nL: int):
         return None
     if t.get("context") != ctx or t.get("layers") != nL:
         return None
-    return t.get("bytes_per_launch")
+    return t.get("bytes_per_token")
 
 
 def cpu_baseline(L, committed, qpos, q, nL, seconds, log):

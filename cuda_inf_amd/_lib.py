@@ -64,6 +64,7 @@ SIGNATURES = {
     "cia_layer_append": (_I, [_P, _P, _P, _I, _I, _P]),
     "cia_decode_loop": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _P, _P]),
     "cia_decode_loop_ex": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _I, _P, _P]),
+    "cia_decode_loop_runs": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _F, _I, _I, _P, _P]),
     "cia_decode_fault": (_I, [_P, ctypes.c_int64, _P]),
     # include/cuda_inf_model.h
     "cia_index_read": (_I, [ctypes.c_char_p, _P, ctypes.c_int64, _P]),

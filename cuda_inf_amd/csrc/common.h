@@ -49,6 +49,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// a - b, never fused with the multiply that produced a: the result is the
+// same whether or not the compiler can see that product (a select it folds
+// away would otherwise decide between v_fma and v_mul + v_sub)
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
 
 // ---------------------------------------------------------------- E4M3
 // gfx950's fp8 conversions use the OCP E4M3 format (bias 7, max 448,

@@ -828,7 +828,7 @@ __global__ __launch_bounds__(kDecThreads) void k_decode(DecArgs a) {
       }
       x = live ? x : -1e30f;
       const float M = wave_max_fast(x);
-      const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
+      const float p = live ? __builtin_amdgcn_exp2f(sub_rn(x, M)) : 0.f;
       const float L = wave_sum_fast(p);
       // ---- P V (tail_pv: rows summed per parity, then even + odd)
       if constexpr (!kCommit) {

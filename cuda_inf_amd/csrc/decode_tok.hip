@@ -111,6 +111,8 @@ struct TokLayer {
 struct TokArgs {
   TokLayer L[kTokMaxLayers];
   int nl, committed, qpos;
+  int ntok;        // tokens (decode steps) in this launch: qpos, qpos + 1, ...
+  int qs, kvs;     // token t's q / out rows at L[li].q + t qs, its k / v at + t kvs
   float scale, eps;
   float* part;     // [8][kMaxRanges][4][kPartRow]
   uint32_t* tick;  // [layer][8][4], kCntStride apart
@@ -163,8 +165,12 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
   const int np = r <= ne ? kFpWaves + 1 : kFpWaves;         // wave partials in LDS
   const float qscale = a.scale * kLog2e;
   const int nl = a.nl, qpos = a.qpos, committed = a.committed;
-  const int tt = qpos + 1 - committed;                       // tail keys, the fresh one last
-  const bool commit = tt == G;
+  // steps: token tok's layer li is step tok * nl + li (one token with the
+  // producers: their rotation is per position)
+  const int ntok = kPrep ? 1 : a.ntok, ns = ntok * nl;
+  // the step each wave is at (its role loop sets them): token, tail keys
+  // of the token (the fresh one last) and step
+  int tok = 0, tt = qpos + 1 - committed, step = 0;
 
   // ---- control wave: the RoPE rotation of lane l at qpos (the same for
   // every layer) into LDS for the waves that prepare rows, and the zero row
@@ -361,8 +367,8 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
 
   // control wave: wait for layer li - 1, then layer li's q rows (and fresh token) into LDS
   auto control_wait = [&](int li) __attribute__((always_inline)) {
-    // layer li - 1 complete (every output row stored): this workgroup's go
-    // word reaches li (written by the count that completed the layer); read
+    // step - 1 complete (every output row stored): this workgroup's go word
+    // reaches step (written by the count that completed that step); read
     // on the scalar path, so the polls do not queue behind the V DMAs the
     // FP8 waves sent at B3 (56.3-56.5 -> 54.9-55.1 us per token at 32 768
     // keys x 6 layers against the vector poll, A/B on one box)
@@ -371,15 +377,15 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     int it = 0;
     for (;;) {
       const uint32_t v = scalar_poll(gw);
-      if (v >= (uint32_t)li) break;
+      if (v >= (uint32_t)step) break;
       if (++it > kSpinMax) {
         if (l == 0) __hip_atomic_fetch_or(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    // the last layer's word is written no more: back to zero for the next launch
-    if (li == nl - 1 && l == 0) __hip_atomic_store(gw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last step's word is written no more: back to zero for the next launch
+    if (step == ns - 1 && l == 0) __hip_atomic_store(gw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   // layer li's q rows i0..i1-1 of the kv head (and, with `fresh` on range
   // 0, the fresh token) into LDS, prepared when the producers run here
@@ -388,11 +394,11 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     uint16_t qr[GQA];
 #pragma unroll
     for (int i = 0; i < GQA; i++)
-      if (i >= i0 && i < i1) qr[i] = Ly.q[(g * GQA + i) * D + l];
+      if (i >= i0 && i < i1) qr[i] = Ly.q[(size_t)tok * a.qs + (g * GQA + i) * D + l];
     uint16_t kr = 0, vr = 0, qwv = 0, kwv = 0;
     if (fresh && r == 0) {
-      kr = Ly.knew[g * D + l];
-      vr = Ly.vnew[g * D + l];
+      kr = Ly.knew[(size_t)tok * a.kvs + g * D + l];
+      vr = Ly.vnew[(size_t)tok * a.kvs + g * D + l];
     }
     if constexpr (kPrep) {
       qwv = Ly.qw[l];
@@ -443,10 +449,13 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       vpre = false;
     }
+    // the next unit: this layer's, or the next step's first (layer li + 1,
+    // or layer 0 of the next token; the same groups, no commit between)
+    const int nli = li + 1 == nl ? 0 : li + 1;
     for (int u = g0;; u += 2) {
       const bool lastu = u + 2 >= g1;
-      const int lin = lastu ? li + 1 : li, un = lastu ? g0 : u + 2;
-      if (lin < nl && (kXPre || !lastu)) {
+      const int lin = lastu ? nli : li, un = lastu ? g0 : u + 2;
+      if ((!lastu || step + 1 < ns) && (kXPre || !lastu)) {
         if (vpre) unit(li, u, lin, un, T_{}, T_{});
         else unit(li, u, lin, un, T_{}, F_{});
         // the next unit's V, once this unit's P V has read the buffer (the
@@ -554,7 +563,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     }
     x = live ? x : -1e30f;
     const float M = wave_max_fast(x);
-    const float p = live ? __builtin_amdgcn_exp2f(x - M) : 0.f;
+    const float p = live ? __builtin_amdgcn_exp2f(sub_rn(x, M)) : 0.f;
     const float L = wave_sum_fast(p);
     // ---- P V (the fresh V row from LDS)
     const uint32_t fv = *(const uint32_t*)(svn + 2 * (l & 31));
@@ -609,23 +618,26 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
   // else it is stored for the final merge and a ticket taken: true when this
   // workgroup holds the head's last partial (then merge_finish runs here).
   auto count_done = [&](int li) __attribute__((always_inline)) {
-    // the output row stored: counted in layer li's done counter; the count
-    // that completes the layer resets the counter and (but after the last
-    // layer) sets every workgroup's go word to li + 1
+    // the output row stored: counted in layer li's done counter, which
+    // counts on through the launch's tokens (token tok's layer li is
+    // complete at (tok + 1) kDoneTarget; no reset between two uses, so none
+    // to order before the go words).  The count that completes the step
+    // sets every workgroup's go word to step + 1 (but after the last), and
+    // on the last token it resets the counter for the next launch.
     stores_acked();
     uint32_t old = 0;
     if (l == 0)
       old = __hip_atomic_fetch_add(a.done + li * kCntStride, 1u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
-    if (old == kDoneTarget - 1) {
-      if (l == 0)
+    if (old == (uint32_t)(tok + 1) * kDoneTarget - 1) {
+      if (l == 0 && tok == ntok - 1)
         __hip_atomic_store(a.done + li * kCntStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (li + 1 < nl) {
+      if (step + 1 < ns) {
         // (agent-coherent stores: the relaxed agent-scope atomic store's form)
         const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.go);
         for (int x = l; x < (int)gridDim.x; x += 64)
-          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(li + 1), rg, x * (kTokGoStride * 4), 0, kCoherent);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(step + 1), rg, x * (kTokGoStride * 4), 0, kCoherent);
       }
     }
 #ifdef CIA_TIMELINE
@@ -658,7 +670,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // (the LDS reads done before the next layer's writes)
     bool last = false;
     if (R == 1) {
-      __builtin_amdgcn_raw_buffer_store_b16(f2h(Oa * (1.0f / L)), buf_rsrc(Ly.out), d * 2, h * D * 2,
+      __builtin_amdgcn_raw_buffer_store_b16(f2h(Oa * (1.0f / L)), buf_rsrc(Ly.out + (size_t)tok * a.qs), d * 2, h * D * 2,
                                             kCoherent);
       count_done(li);
     } else {
@@ -692,7 +704,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     // (the resource ends at the R partials: reads past them return zero)
     const __amdgpu_buffer_rsrc_t rs =
         buf_rsrc(a.part + (size_t)g * kMaxRanges * kPartF, (uint32_t)R * (GQA * kPartRow * 4));
-    const __amdgpu_buffer_rsrc_t ro = buf_rsrc(Ly.out);
+    const __amdgpu_buffer_rsrc_t ro = buf_rsrc(Ly.out + (size_t)tok * a.qs);
     // lane p weighs partial p, then lane d sums dim d (the row reads go
     // out together; the weights come from lane p).  NP: 32 partials, or
     // kMaxRanges for the unequal ranges; the terms past R weigh 0.
@@ -760,8 +772,14 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       if (w >= kMergeW0) open_rows(li, w - kMergeW0, w - kMergeW0 + 1, w == kMergeW0);
     }
   };
+  // Each role's loop runs the steps in order: token tok = st / nl, layer
+  // li = st % nl (one token per launch but in the decode loop's runs of
+  // tokens without a commit between them; only the last may commit).
   if (fp8w) {
-    for (int li = 0; li < nl; li++) {
+    for (int st = 0; st < ns; st++) {
+      tok = kPrep ? 0 : st / nl;
+      const int li = kPrep ? st : st - tok * nl;
+      step = st;
       b0();
       b1();
       TL_STAMP(8 * li);
@@ -769,17 +787,20 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       b2();
       TL_STAMP(8 * li + 4);
       b3();
-      if (kXPre && li + 1 < nl) {
+      if (kXPre && st + 1 < ns) {
         __builtin_amdgcn_sched_barrier(0);
-        issue(a.L[li + 1].vc8, g0, vw);
+        issue(a.L[li + 1 == nl ? 0 : li + 1].vc8, g0, vw);
         __builtin_amdgcn_sched_barrier(0);
         TL_STAMP(8 * li + 6);
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (nothing left in flight)
   } else if (w == kCtlW) {
-    for (int li = 0; li < nl; li++) {
-      if (li > 0) control_wait(li);
+    for (int st = 0; st < ns; st++) {
+      tok = kPrep ? 0 : st / nl;
+      const int li = kPrep ? st : st - tok * nl;
+      step = st;
+      if (st > 0) control_wait(li);
       if constexpr (kPrep)
         prep_part(li);
       else
@@ -792,10 +813,11 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       b3();
     }
   } else if (tailw) {
-    // (one loop for the step that commits the group, one for the others:
+    // (one loop for the token that commits the group, one for the others:
     // their registers never meet)
     auto tail_loop = [&](auto commit_tag) __attribute__((always_inline)) {
       for (int li = 0; li < nl; li++) {
+        step = tok * nl + li;
         tail_load(li, commit_tag);
         prep_part(li);
         b1();
@@ -804,15 +826,31 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
         b2();
         TL_STAMP(8 * li + 1);
         if (w >= kMergeW0) merge_part(li);
+        // (wave 8 wrote the fresh row: stored before B3, so the next
+        // token's tail loads, after it, read it)
+        if (w == kFpWaves) __builtin_amdgcn_s_waitcnt(0x0F70);
         b3();
       }
     };
-    if (commit)
-      tail_loop(T_{});
-    else
-      tail_loop(F_{});
+    if constexpr (kPrep) {
+      if (tt == G)
+        tail_loop(T_{});
+      else
+        tail_loop(F_{});
+    } else {
+      // (only the last token may fill the group)
+      for (tok = 0; tok < ntok; tok++) {
+        tt = qpos + tok + 1 - committed;
+        if (tt == G) break;
+        tail_loop(F_{});
+      }
+      if (tok < ntok) tail_loop(T_{});
+    }
   } else {
-    for (int li = 0; li < nl; li++) {
+    for (int st = 0; st < ns; st++) {
+      tok = kPrep ? 0 : st / nl;
+      const int li = kPrep ? st : st - tok * nl;
+      step = st;
       prep_part(li);
       b1();
       TL_STAMP(8 * li);
@@ -889,16 +927,30 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok_fits(const c
   return occ[dev] > 0;
 }
 
-// One decode step of nl layers (cia_decode_tok_fits true): q / out rows of
-// layer j at q + j * 2048 / out + j * 2048, the fresh k / v at k + j * 512,
-// v + j * 512 (the decode loop's [layer] rows of one step), position past.
-// The workspace is layer 0's ws_decode.
+// ntok decode steps of nl layers (cia_decode_tok_fits true at past) in one
+// launch, positions past .. past + ntok - 1: token t's q / out rows of layer
+// j at q + t qs + j * 2048 / out + t qs + j * 2048, its fresh k / v at
+// k + t kvs + j * 512, v + t kvs + j * 512 (the decode loop's [step][layer]
+// rows).  Token t + 1's layer 0 is scored after token t's last layer's
+// output is stored, as layer j + 1 after layer j.  Only the last token may
+// fill the group (the caller splits its runs there: the groups of the FP8
+// waves stay the same), and ntok > 1 needs prepared q / k (no producers:
+// their rotation is per position).  The workspace is layer 0's ws_decode.
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok(
     const cia_layer* L, int nl, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-    uint16_t* out, int past, float scale, void* stream) {
+    uint16_t* out, int past, float scale, int ntok, int64_t qs, int64_t kvs, void* stream) {
   if (!q || !k || !v || !out) return CIA_ERR_NULL;
+  if (ntok < 1 || ntok > G || (ntok > 1 && L[0].qw)) return CIA_ERR_ARG;
   if (!aligned(q, 2) || !aligned(k, 2) || !aligned(v, 2) || !aligned(out, 2)) return CIA_ERR_ALIGN;
   const int committed = L[0].committed, ng = committed / G, R = dec_ranges(ng);
+  if (ntok > 1) {
+    // the run ends at the step that fills the group, inside every layer
+    if (past - committed + ntok > G || qs < 0 || kvs < 0 || qs > INT32_MAX / G ||
+        kvs > INT32_MAX / G)
+      return CIA_ERR_ARG;
+    for (int j = 0; j < nl; j++)
+      if (past + ntok > L[j].maxT) return CIA_ERR_ARG;
+  }
   TokArgs ta{};
   for (int j = 0; j < nl; j++) {
     TokLayer& t = ta.L[j];
@@ -918,6 +970,9 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok(
   ta.nl = nl;
   ta.committed = committed;
   ta.qpos = past;
+  ta.ntok = ntok;
+  ta.qs = (int)qs;
+  ta.kvs = (int)kvs;
   ta.scale = scale;
   ta.eps = L[0].eps;
   char* ws = (char*)L[0].ws_decode;

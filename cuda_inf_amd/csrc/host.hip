@@ -36,7 +36,7 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok_fits(const c
 
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok(
     const cia_layer* L, int nl, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-    uint16_t* out, int past, float scale, void* stream);
+    uint16_t* out, int past, float scale, int ntok, int64_t qs, int64_t kvs, void* stream);
 
 extern "C" __attribute__((visibility("hidden"))) const void* cia_qk_prep_desc(
     const uint16_t* qw, const uint16_t* kw, float eps, float theta);
@@ -321,12 +321,30 @@ extern "C" int cia_layer_append(cia_layer* L, const uint16_t* k, const uint16_t*
   return S ? group64_append(L, k, v, S, past, stream) : CIA_OK;
 }
 
-extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_t* q,
-                                  const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
-                                  int steps, float scale, int layers_per_launch, void** events,
-                                  void* stream) {
+// Steps pos, pos + 1, .. (at most max_steps) that one k_decode_tok launch
+// can run: the layers qualify at pos, and the run stops at the step whose
+// token fills the group and at every layer's capacity.  0: none.
+static int decode_run(const cia_layer* layers, int n_layers, int pos, int max_steps) {
+  if (max_steps < 2 || !cia_decode_tok_fits(layers, n_layers, pos)) return 0;
+  const int c = layers[0].committed;  // (the same in every layer: fits)
+  int run = std::min(max_steps, CIA_KVGROUP - (pos - c));
+  for (int j = 0; j < n_layers; j++) run = std::min(run, layers[j].maxT - pos);
+  if (pos + run - 1 - c == CIA_KVGROUP - 1) {
+    bool fits = true;
+    for (int j = 0; j < n_layers; j++) fits = fits && c + CIA_KVGROUP <= layers[j].maxT;
+    if (!fits) run--;  // (the commit would not fit: the run stops before it)
+  }
+  return run;
+}
+
+extern "C" int cia_decode_loop_runs(cia_layer* layers, int n_layers, const uint16_t* q,
+                                    const uint16_t* k, const uint16_t* v, uint16_t* out,
+                                    int past, int steps, float scale, int layers_per_launch,
+                                    int tokens_per_launch, void** events, void* stream) {
   if (!layers || !q || !k || !v || !out) return CIA_ERR_NULL;
-  if (n_layers < 1 || steps < 0 || past < 0 || layers_per_launch < 0) return CIA_ERR_ARG;
+  if (n_layers < 1 || steps < 0 || past < 0 || layers_per_launch < 0 || tokens_per_launch < 0)
+    return CIA_ERR_ARG;
+  const int tok_max = tokens_per_launch == 0 ? CIA_KVGROUP : std::min(tokens_per_launch, CIA_KVGROUP);
   for (int l = 0; l < n_layers; l++) {
     const int st = prep_check(&layers[l]);
     if (st) return st;
@@ -337,6 +355,25 @@ extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_
   hipStream_t s = (hipStream_t)stream;
   for (int i = 0; i < steps; i++) {
     const int pos = past + i;
+    // A run of steps (at most tok_max) in one launch when every layer of a
+    // step goes in one launch, no per-step events are asked for and q / k
+    // come prepared: the steps up to the one that fills the group (it ends
+    // the run; the next run's FP8 groups include it).
+    if (!events && per > 1 && n_layers <= per && !layers[0].qw && tok_max > 1) {
+      const int run = decode_run(layers, n_layers, pos, std::min(steps - i, tok_max));
+      if (run > 1) {
+        const size_t r = (size_t)i * n_layers;
+        const int st = cia_decode_tok(layers, n_layers, q + r * qrow, k + r * krow, v + r * krow,
+                                      out + r * qrow, pos, scale, run, (int64_t)n_layers * qrow,
+                                      (int64_t)n_layers * krow, stream);
+        if (st) return st;
+        const int last = pos + run - 1;
+        for (int j = 0; j < n_layers; j++)
+          if (last - layers[j].committed == CIA_KVGROUP - 1) layers[j].committed += CIA_KVGROUP;
+        i += run - 1;
+        continue;
+      }
+    }
     for (int l = 0; l < n_layers;) {
       const size_t r = (size_t)i * n_layers + l;
       int st;
@@ -347,7 +384,7 @@ extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_
           for (int j = 0; j < chunk; j++)
             if ((st = hip_check(hipEventRecord((hipEvent_t)events[3 * (r + j)], s)))) return st;
         st = cia_decode_tok(&layers[l], chunk, q + r * qrow, k + r * krow, v + r * krow,
-                            out + r * qrow, pos, scale, stream);
+                            out + r * qrow, pos, scale, 1, 0, 0, stream);
         if (st) return st;
         if (events)
           for (int j = 0; j < chunk; j++)
@@ -391,11 +428,19 @@ extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_
   return CIA_OK;
 }
 
+extern "C" int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_t* q,
+                                  const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
+                                  int steps, float scale, int layers_per_launch, void** events,
+                                  void* stream) {
+  return cia_decode_loop_runs(layers, n_layers, q, k, v, out, past, steps, scale,
+                              layers_per_launch, 0, events, stream);
+}
+
 extern "C" int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
                                const uint16_t* k, const uint16_t* v, uint16_t* out, int past,
                                int steps, float scale, void** events, void* stream) {
-  return cia_decode_loop_ex(layers, n_layers, q, k, v, out, past, steps, scale, 0, events,
-                            stream);
+  return cia_decode_loop_runs(layers, n_layers, q, k, v, out, past, steps, scale, 0, 0, events,
+                              stream);
 }
 
 // ---------------------------------------------------------------- attention branch

@@ -451,15 +451,31 @@ int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
  * In one launch layer l + 1's scores start only after every output row of
  * layer l is stored (its q would be computed from them), while its FP8 K/V
  * already stream in; outputs and cache bytes are bit-identical to the
- * per-layer launches.  The workspace is the first layer's ws_decode.  With
- * events, every layer of such a launch has events[3r] recorded before it
- * and events[3r+1], events[3r+2] after it.  The in-launch wait between
- * layers is bounded: if the grid was not resident at once it gives up and
- * sets the workspace's fault word (cia_decode_fault) rather than hang. */
+ * per-layer launches.  When all the layers of a step go in one launch, no
+ * events are given and q / k come prepared (no QK producers), consecutive
+ * steps run in that same launch too, up to the step whose token fills a
+ * group (a run of at most 64 steps): step t + 1's first layer is scored only
+ * after step t's last layer has stored its output, as between layers.  The
+ * workspace is the first layer's ws_decode.  With events, every step is a
+ * launch of its own, and every layer of such a launch has events[3r]
+ * recorded before it and events[3r+1], events[3r+2] after it.  The
+ * in-launch wait between layers is bounded: if the grid was not resident
+ * at once it gives up and sets the workspace's fault word
+ * (cia_decode_fault) rather than hang. */
 int cia_decode_loop_ex(cia_layer* layers, int n_layers, const uint16_t* q,
                        const uint16_t* k, const uint16_t* v, uint16_t* out,
                        int past, int steps, float scale,
                        int layers_per_launch, void** events, void* stream);
+
+/* cia_decode_loop_ex with the steps per launch bounded as well:
+ * tokens_per_launch 1 launches every step on its own (no runs), n >= 2 at
+ * most n steps per run, 0 (cia_decode_loop_ex's choice) runs up to each
+ * group fill.  Outputs and cache bytes do not depend on it.  No
+ * counterpart in the reference (its decode launches per layer). */
+int cia_decode_loop_runs(cia_layer* layers, int n_layers, const uint16_t* q,
+                         const uint16_t* k, const uint16_t* v, uint16_t* out,
+                         int past, int steps, float scale, int layers_per_launch,
+                         int tokens_per_launch, void** events, void* stream);
 
 /* Reads (synchronously) the fault word of a decode workspace: nonzero when a
  * one-launch multi-layer step gave up waiting for a previous layer (its

@@ -80,6 +80,10 @@ FAKE = 0x10000  # aligned non-null address: validation must fail before any use
                                    FAKE, FAKE, FAKE, None), 3),
     (lambda L: L.cia_qkv_proj_int4(FAKE, FAKE, FAKE, 64, FAKE, FAKE, FAKE, FAKE, 16, 128, 1,
                                    FAKE, None, FAKE, None), 1),
+    (lambda L: L.cia_decode_loop_runs(FAKE, 1, *([FAKE] * 4), 100, 1, 0.125, 0, -1, None, None), 3),
+    (lambda L: L.cia_decode_loop_runs(FAKE, 0, *([FAKE] * 4), 100, 1, 0.125, 0, 0, None, None), 3),
+    (lambda L: L.cia_decode_loop_runs(None, 1, *([FAKE] * 4), 100, 1, 0.125, 0, 0, None, None), 1),
+    (lambda L: L.cia_decode_loop_ex(FAKE, 1, *([FAKE] * 4), 100, -1, 0.125, 0, None, None), 3),
     (lambda L: L.cia_e4m3_encode_range(0, -1, FAKE, None), 3),
     (lambda L: L.cia_e4m3_encode_range(0, 16, FAKE + 8, None), 2),
 ])

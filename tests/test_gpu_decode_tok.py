@@ -16,6 +16,11 @@ oracle:
 - 6 layers x 64 steps at 32 768 keys crossing the commit of group 512:
   every step's output within 2e-3 + 1e-3 |ref| of the oracle's fp32 result,
   the committed bytes and scales and the tail identical;
+- runs of steps in one launch (the decode loop's default without events:
+  consecutive tokens up to the one that fills a group) against one launch
+  per token and against runs of at most 5 tokens: the same cache bytes and
+  bit-identical outputs, through group commits, at 4155, 32 763, 40 000
+  and 65 600 keys;
 - the workspace's fault word stays 0 (no bounded wait gave up).
 """
 import ctypes
@@ -231,3 +236,44 @@ def test_layer_counts_and_chunks(orc, cia, dev, nL, n0):
             x, y = getattr(la[l], name), getattr(lb[l], name)
             assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), (l, name)
     assert np.array_equal(_u16(oa), _u16(ob)), "outputs not bit-identical"
+
+
+@pytest.mark.parametrize("n0,nL,steps", [(4155, 6, 70), (32763, 6, 12), (40000, 2, 70),
+                                         (65600, 3, 66)])
+def test_runs_match_one_token_launches(cia, dev, n0, nL, steps):
+    """cia_decode_loop_runs with tokens_per_launch 0 (runs up to each group
+    fill: at 4155 keys runs of 5, 64 and 1 tokens), 5 (runs of at most 5)
+    and 1 (one launch per token): the cache bytes and the outputs of every
+    step bit-identical, and the fault word 0.  A run only moves launch
+    boundaries; each step's arithmetic is the same."""
+    from cuda_inf_amd import _lib
+    print(f"runs vs one token per launch: {n0} keys, {nL} layers, {steps} steps", flush=True)
+    maxT = n0 + steps + 64
+    g = np.random.default_rng(31 + n0)
+    q = (g.standard_normal((steps, nL, 32, 64)) * 2).astype(np.float16)
+    k = (g.standard_normal((steps, nL, 8, 64)) * 2).astype(np.float16)
+    v = g.standard_normal((steps, nL, 8, 64)).astype(np.float16)
+    qd, kd, vd = _t16(q, dev), _t16(k, dev), _t16(v, dev)
+    runs = []
+    for tpl in (1, 0, 5):
+        layers = _layers(dev, n0, nL, 800, maxT)
+        arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+        out = torch.zeros((steps, nL, 32, 64), dtype=torch.float16, device=dev)
+        _lib.call("cia_decode_loop_runs", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                  out.data_ptr(), n0, steps, 0.125, 0, tpl, None,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert _fault(layers[0]) == 0, f"a bounded wait gave up (tokens_per_launch {tpl})"
+        runs.append((layers, arr, out))
+        print(f"  tokens_per_launch={tpl} done", flush=True)
+    la, aa, oa = runs[0]
+    for lb, ab, ob in runs[1:]:
+        for l in range(nL):
+            assert aa[l].committed == ab[l].committed == (n0 + steps) // 64 * 64
+            for name in NAMES:
+                x, y = getattr(la[l], name), getattr(lb[l], name)
+                assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), (l, name)
+        ua, ub = _u16(oa), _u16(ob)
+        if not np.array_equal(ua, ub):
+            s, l = np.argwhere((ua != ub).any(axis=(2, 3)))[0]
+            raise AssertionError(f"outputs differ first at step {s} (key {n0 + s}) layer {l}")
