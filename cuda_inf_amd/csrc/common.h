@@ -95,6 +95,26 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 __device__ __forceinline__ float quant_scale(float amax) {
   return amax / 448.0f + 1e-12f;
 }
+// x / s as the IEEE division rounds it, for a scale s = quant_scale(amax)
+// and r = 1 / s (IEEE), with s passed through quant_div_s: q0 = x r, the
+// exact remainder e = x - q0 s by fma, one correction q0 + e r (Markstein's
+// final step), and x's sign back for x = -0 (the correction gives +0
+// there).  Three operations instead of a division's ten, with r computed
+// once per scale.  Equal to x / s in every bit for every fp16 x and the
+// scale of every finite fp16 amax (2.0e9 pairs), and for every finite x
+// when amax is infinite (an inf in the group: s = inf, r = 0, passed as
+// s = 0, gives x r = +-0 as x / inf does); an infinite x there gives a NaN
+// of its own sign.  All of it is checked on the CPU by
+// tests/quant_div_check.c.
+__device__ __forceinline__ float quant_div_s(float s) {
+  return s == __builtin_inff() ? 0.f : s;
+}
+__device__ __forceinline__ float quant_div(float x, float s, float r) {
+#pragma clang fp contract(off)
+  const float q0 = x * r;
+  const float e = __builtin_fmaf(-q0, s, x);
+  return __builtin_copysignf(__builtin_fmaf(e, r, q0), x);
+}
 
 // ---------------------------------------------------------------- exp
 // Deterministic exp used for the H2O attention mass: Cody-Waite reduction by

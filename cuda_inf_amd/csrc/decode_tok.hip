@@ -542,14 +542,17 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       const uint16_t skh = f2h(sck);
       const float kdq = h2f(skh);
       uint8_t* krow8 = Ly.kc8 + ((size_t)(committed + l) * NKV + g) * D;
+      // x / sck by quant_div, the reciprocal taken once
+      const float rk = 1.0f / sck, sk = quant_div_s(sck);
       float sacc = 0.f;
 #pragma unroll
       for (int j = 0; j < 16; j++) {
         const u32x4 src = kq[j >> 1];
         const int e0 = (j & 1) * 2;
-        const uint32_t kb = e4m3x4(h2f((uint16_t)src[e0]) / sck, h2f((uint16_t)(src[e0] >> 16)) / sck,
-                                   h2f((uint16_t)src[e0 + 1]) / sck,
-                                   h2f((uint16_t)(src[e0 + 1] >> 16)) / sck);
+        const uint32_t kb = e4m3x4(quant_div(h2f((uint16_t)src[e0]), sk, rk),
+                                   quant_div(h2f((uint16_t)(src[e0] >> 16)), sk, rk),
+                                   quant_div(h2f((uint16_t)src[e0 + 1]), sk, rk),
+                                   quant_div(h2f((uint16_t)(src[e0 + 1] >> 16)), sk, rk));
         const f16x8 q8 = *(const f16x8*)(qrow + 8 * (j >> 1));
         const int o4 = (j & 1) * 4;
         sacc = __builtin_fmaf((float)q8[o4 + 0], e4m3_to_f32<0>(kb) * kdq, sacc);
@@ -590,12 +593,13 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       const float scv = quant_scale(wave_max_fast(av));
       const uint16_t svh = f2h(scv);
       const float vdq = h2f(svh);
+      const float rv = 1.0f / scv, sv = quant_div_s(scv);
       // P V in the order of tail_pv: even rows, odd rows, then their sum
       float oe = 0.f, oo = 0.f;
 #pragma unroll
       for (int k = 0; k < G; k++) {
         const float vk = h2f((uint16_t)(vp[k >> 1] >> (16 * (k & 1))));
-        const uint32_t vb = e4m3x2(vk / scv, 0.f) & 0xFFu;
+        const uint32_t vb = e4m3x2(quant_div(vk, sv, rv), 0.f) & 0xFFu;
         if (i == 0) Ly.vc8[((size_t)(committed + k) * NKV + g) * D + l] = (uint8_t)vb;
         const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), k));
         if (k & 1) oo = __builtin_fmaf(pk, e4m3_to_f32<0>(vb) * vdq, oo);
@@ -826,9 +830,9 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
         b2();
         TL_STAMP(8 * li + 1);
         if (w >= kMergeW0) merge_part(li);
-        // (wave 8 wrote the fresh row: stored before B3, so the next
-        // token's tail loads, after it, read it)
-        if (w == kFpWaves) __builtin_amdgcn_s_waitcnt(0x0F70);
+        // (wave 8 wrote the fresh row: stored before B3 when a next token
+        // follows in this launch, so that its tail loads, after B3, read it)
+        if (w == kFpWaves && tok + 1 < ntok) __builtin_amdgcn_s_waitcnt(0x0F70);
         b3();
       }
     };

@@ -216,47 +216,6 @@ __device__ __forceinline__ f32x2 tail_pv(const uint32_t (&vr)[G / 2], float p, i
   const f32x2 a = swap32(o0), b = swap32(o1);
   return f32x2{a[0] + a[1], b[0] + b[1]};
 }
-// The group the fresh token completes: rows 0..62 in vr, row 63 (fv) the
-// fresh one.  V quantised with its group scale (kv_commit_group,
-// engine.cu:202-228): the bytes written to the group's rows of vc8 when
-// `write`, the scale returned in *svh, and P V over the FP8 values, summed
-// as tail_pv.  row0: the group's first key.
-__device__ __forceinline__ f32x2 tail_commit_v(const uint32_t (&vr)[G / 2], float p, uint32_t fv,
-                                               uint8_t* vc8, int row0, int g, bool write,
-                                               uint16_t* svh) {
-  const int l = threadIdx.x & 63, j = l & 31, h = l >> 5;
-  // the group's rows of kv head g: the row goes in the scalar offset
-  const __amdgpu_buffer_rsrc_t rc = buf_rsrc(vc8 + ((size_t)row0 * NKV + g) * D);
-  const int co = h * (NKV * D) + 2 * j;
-  float av = 0.f;
-#pragma unroll
-  for (int k = 0; k < G / 2; k++) {
-    const uint32_t v = k == G / 2 - 1 && h ? fv : vr[k];
-    av = __builtin_fmaxf(av, __builtin_fmaxf(__builtin_fabsf(h2f((uint16_t)v)),
-                                             __builtin_fabsf(h2f((uint16_t)(v >> 16)))));
-  }
-  const float scv = quant_scale(wave_max_fast(av));
-  *svh = f2h(scv);
-  const float vdq = h2f(*svh);
-  float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-  for (int k = 0; k < G / 2; k++) {
-    const uint32_t v = k == G / 2 - 1 && h ? fv : vr[k];
-    const uint32_t vb = e4m3x2(h2f((uint16_t)v) / scv, h2f((uint16_t)(v >> 16)) / scv);
-    if (write) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)vb, rc, co, 2 * k * (NKV * D), 0);
-    const float pe = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 2 * k));
-    const float po = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 2 * k + 1));
-    const float pr = h ? po : pe;
-    o0 = __builtin_fmaf(pr, e4m3_to_f32<0>(vb) * vdq, o0);
-    o1 = __builtin_fmaf(pr, e4m3_to_f32<1>(vb) * vdq, o1);
-    // (one row pair at a time: the step runs once a group, and its
-    // divisions scheduled together would hold more registers than a wave has)
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  const f32x2 a = swap32(o0), b = swap32(o1);
-  return f32x2{a[0] + a[1], b[0] + b[1]};
-}
-
 // ---------------------------------------------------------------- host side
 // compute units of the current device (0 if unknown)
 inline int device_cus() {
