@@ -266,7 +266,7 @@ def main():
     floor_bytes = 2 * arr[0].committed * NKV * D
     floor_gbps = floor_bytes / (floor_us * 1e-6) / 1e9
     log(f"plain read of the same bytes: {floor_us:.2f} us per layer, {floor_gbps:.0f} GB/s "
-        f"({us_tok / (nL * floor_us):.2f}x the decode's time per token)")
+        f"(the decode takes {us_tok / (nL * floor_us):.2f}x its time per token)")
 
     # ---- cold: evict the KV from the 256 MB Infinity Cache before every token
     # by reading 1 GiB of other data (a read leaves no dirty lines behind)
