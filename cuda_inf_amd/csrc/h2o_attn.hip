@@ -234,7 +234,8 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
       if (wave_id() == 0) {
         const float sck = quant_scale(wave_max_fast(__builtin_fabsf(tk)));
         const float scv = quant_scale(wave_max_fast(__builtin_fabsf(tv)));
-        const uint32_t kb = e4m3x2(tk / sck, 0.f) & 0xFFu, vb = e4m3x2(tv / scv, 0.f) & 0xFFu;
+        const uint32_t kb = e4m3x2(quant_div(tk, quant_div_s(sck), 1.0f / sck), 0.f) & 0xFFu;
+        const uint32_t vb = e4m3x2(quant_div(tv, quant_div_s(scv), 1.0f / scv), 0.f) & 0xFFu;
         newkv[0][lane] = (uint8_t)kb;
         newkv[1][lane] = (uint8_t)vb;
         const size_t o = ((size_t)slot * NKV + kvh) * D + lane;

@@ -77,11 +77,15 @@ __device__ __forceinline__ void commit_group_rows(const uint16_t* __restrict__ k
     ksc[grp * NKV + h] = f2h(sck);
     vsc[grp * NKV + h] = f2h(scv);
   }
+  // x / scale by quant_div, the reciprocals taken once
+  const float rk = 1.0f / sck, sk = quant_div_s(sck), rv = 1.0f / scv, sv = quant_div_s(scv);
   u32x4 kb, vb;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    kb[j] = e4m3x4(kf[4 * j] / sck, kf[4 * j + 1] / sck, kf[4 * j + 2] / sck, kf[4 * j + 3] / sck);
-    vb[j] = e4m3x4(vf[4 * j] / scv, vf[4 * j + 1] / scv, vf[4 * j + 2] / scv, vf[4 * j + 3] / scv);
+    kb[j] = e4m3x4(quant_div(kf[4 * j], sk, rk), quant_div(kf[4 * j + 1], sk, rk),
+                   quant_div(kf[4 * j + 2], sk, rk), quant_div(kf[4 * j + 3], sk, rk));
+    vb[j] = e4m3x4(quant_div(vf[4 * j], sv, rv), quant_div(vf[4 * j + 1], sv, rv),
+                   quant_div(vf[4 * j + 2], sv, rv), quant_div(vf[4 * j + 3], sv, rv));
   }
   const size_t dst = ((size_t)(dst_tok_base + tok) * NKV + h) * D + c;
   *(u32x4*)(kc8 + dst) = kb;
@@ -197,7 +201,8 @@ __device__ __forceinline__ void quant_write_row(const uint16_t* __restrict__ k,
   const float mk = wave_max_fast(__builtin_fabsf(kv)), mv = wave_max_fast(__builtin_fabsf(vv));
   const float sck = quant_scale(mk), scv = quant_scale(mv);
   // pack 4 neighbouring lanes' bytes into one dword store
-  uint32_t kb = e4m3x2(kv / sck, 0.f) & 0xFFu, vb = e4m3x2(vv / scv, 0.f) & 0xFFu;
+  uint32_t kb = e4m3x2(quant_div(kv, quant_div_s(sck), 1.0f / sck), 0.f) & 0xFFu;
+  uint32_t vb = e4m3x2(quant_div(vv, quant_div_s(scv), 1.0f / scv), 0.f) & 0xFFu;
   uint32_t kw = kb << (8 * (d & 3)), vw = vb << (8 * (d & 3));
   kw |= __shfl_xor(kw, 1);
   vw |= __shfl_xor(vw, 1);
