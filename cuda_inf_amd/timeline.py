@@ -6,6 +6,13 @@ and its stamps read back (s_memrealtime, 100 MHz), then medians over the
 tokens of each event's time since the launch's first wave started.
 
     python -m cuda_inf_amd.timeline [--ctx 32768] [--layers 6] [--tokens 32]
+    python -m cuda_inf_amd.timeline --run 32 [--tokens 8]
+
+With --run N, each sample is one launch of a run of N tokens from a group
+boundary (N <= 63: no commit inside), and the stamps read back are the
+run's last token's (each token overwrites the one before); times are then
+from that token's first layer open.  A filler call completes the group
+between samples.
 
 Printed per layer: the FP8 waves' "opened" (B1 passed), first unit's K
 landed, V landed, units done, partials-in-LDS (B2) and the next layer's K
@@ -30,7 +37,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prep", action="store_true",
                     help="raw q / k: the QK producers run inside the kernel")
+    ap.add_argument("--run", type=int, default=0,
+                    help="tokens per launch (one run per sample, 2..63); 0: one launch per token")
     a = ap.parse_args()
+    if a.run and not (2 <= a.run <= 63 and a.ctx % 64 == 0 and not a.prep):
+        ap.error("--run needs 2 <= N <= 63, a context that is a multiple of 64 and no --prep")
     from cuda_inf_amd import _lib
     _lib.use_timeline_build()
     import numpy as np
@@ -45,6 +56,9 @@ def main():
     s = torch.cuda.current_stream()
     nL, ctx = a.layers, a.ctx
     n = a.warmup + a.tokens
+    if a.run:
+        a.warmup = min(a.warmup, 2)
+        n = 64 * (a.warmup + a.tokens)
     layers = []
     for l in range(nL):
         L = AttnLayer(ctx + n + 64, nsplit=0, device=dev)
@@ -81,31 +95,42 @@ def main():
     buf = np.zeros(nwg_max * nw * 64, np.uint32)
     qrow, krow = nL * NH * D * 2, nL * NKV * D * 2
     samples = []
-    for i in range(n):
+
+    def decode(i, steps):
         call("cia_decode_loop", arr, nL, q.data_ptr() + i * qrow, kk.data_ptr() + i * krow,
-             vv.data_ptr() + i * krow, out.data_ptr() + i * qrow, ctx + i, 1, 0.125, None,
+             vv.data_ptr() + i * krow, out.data_ptr() + i * qrow, ctx + i, steps, 0.125, None,
              s.cuda_stream)
         torch.cuda.synchronize()
-        if i < a.warmup:
-            continue
-        _lib.check("cia_timeline_read", lib.cia_timeline_read(buf.ctypes.data, buf.nbytes))
-        samples.append(buf.reshape(nwg_max, nw, 64).copy())
+
+    for i in (range(0, n, 64) if a.run else range(n)):
+        decode(i, a.run if a.run else 1)
+        if i >= (64 if a.run else 1) * a.warmup:
+            _lib.check("cia_timeline_read", lib.cia_timeline_read(buf.ctypes.data, buf.nbytes))
+            samples.append(buf.reshape(nwg_max, nw, 64).copy())
+        if a.run:
+            decode(i + a.run, 64 - a.run)  # (the rest of the group and its commit)
     ng = ctx // 64
     R = min(32, ((ng + 15) // 16 + 1) // 2 * 2)
     nwg = 8 * R
     f = ctypes.c_int(-1)
     call("cia_decode_fault", layers[0].ws_decode.data_ptr(), layers[0].ws_decode.numel(),
          ctypes.byref(f))
-    print(f"timeline: ctx {ctx}, {nL} layers, {len(samples)} tokens, {nwg} workgroups; "
+    print(f"timeline: ctx {ctx}, {nL} layers, {len(samples)} "
+          f"{f'runs of {a.run} tokens (their last token)' if a.run else 'tokens'}, {nwg} workgroups; "
           f"fault word {f.value}")
 
     def rel(x, t0):
-        return ((x.astype(np.int64) - t0) % (1 << 32)) / 100.0  # us
+        # signed, in us (the counter wraps at 2^32 ticks of 10 ns)
+        return (((x.astype(np.int64) - t0 + (1 << 31)) % (1 << 32)) - (1 << 31)) / 100.0
+
+    def start(tl):
+        # the launch's first wave, or in a run the last token's first open
+        return int(tl[:, :8, 0].min()) if a.run else int(tl[:, :8, 63].min())
 
     rows = []
     for smp in samples:
         tl = smp[:nwg]
-        t0 = int(tl[:, :8, 63].min())
+        t0 = start(tl)
         res = {}
         for li in range(nL):
             b = 8 * li
@@ -124,9 +149,11 @@ def main():
             res[(li, "merge: partial acked")] = mw[:, :, 2]
             res[(li, "merge: ticket")] = mw[:, :, 3]
             last = tl[:, 9:13, b + 4] != 0
+            if a.run:  # (a last arriver of an earlier token of the run keeps its stamps)
+                last &= rel(tl[:, 9:13, b + 4], t0) > -2.0
             res[(li, "merge: final rows (last)")] = mw[:, :, 4][last] if last.any() else np.zeros(1)
             res[(li, "merge: output counted (last)")] = mw[:, :, 5][last] if last.any() else np.zeros(1)
-            if li > 0:
+            if li > 0 or a.run:
                 res[(li, "control: wait begun")] = ctl[:, 0]
             res[(li, "control: q loaded")] = ctl[:, 1]
             # range 0's tail waves (8-11): rows landed, tail done
@@ -139,7 +166,7 @@ def main():
     # the workgroup that reached "partials in LDS" last in each layer of
     # the last token, with its waves' stamps of that layer
     tl = samples[-1][:nwg]
-    t0 = int(tl[:, :8, 63].min())
+    t0 = start(tl)
     for li in range(nL):
         b = 8 * li
         b2 = rel(tl[:, :8, b + 4], t0).max(axis=1)
@@ -156,7 +183,7 @@ def main():
     hits, tot, gap = 0, 0, []
     for smp in samples:
         tl = smp[:nwg]
-        t0 = int(tl[:, :8, 63].min())
+        t0 = start(tl)
         for li in range(1, nL):
             b2 = rel(tl[:, :8, 8 * li + 4], t0).max(axis=1)
             fm = (tl[:, 9:13, 8 * (li - 1) + 4] != 0).any(axis=1)
