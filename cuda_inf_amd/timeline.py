@@ -132,6 +132,8 @@ def main():
         tl = smp[:nwg]
         t0 = start(tl)
         res = {}
+        if not a.run:
+            res[(0, "workgroup started")] = rel(tl[:, 0, 63], t0)
         for li in range(nL):
             b = 8 * li
             fp8 = rel(tl[:, :8, b:b + 5], t0)            # [wg][wave][5]
