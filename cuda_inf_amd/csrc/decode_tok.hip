@@ -365,8 +365,9 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     vpre = true;
   }
 
-  // control wave: wait for the step before, then the step's q rows (and fresh token) into LDS
-  auto control_wait = [&]() __attribute__((always_inline)) {
+  // control wave: wait for the step before, then the step's q rows (and
+  // fresh token) into LDS; li: the step's layer (the timestamp build's)
+  auto control_wait = [&]([[maybe_unused]] int li) __attribute__((always_inline)) {
     // step - 1 complete (every output row stored): this workgroup's go word
     // reaches step (written by the count that completed that step); read
     // on the scalar path, so the polls do not queue behind the V DMAs the
@@ -804,7 +805,7 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
       tok = kPrep ? 0 : st / nl;
       const int li = kPrep ? st : st - tok * nl;
       step = st;
-      if (st > 0) control_wait();
+      if (st > 0) control_wait(li);
       if constexpr (kPrep)
         prep_part(li);
       else
