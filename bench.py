@@ -370,15 +370,14 @@ def main():
         for l in range(nL):
             arr[l].qw = arr[l].kw = arr[l].prep_ws = None
             arr[l].prep_cap = 0
-        # (the producers rotate at one position per launch: one launch per
-        # token, compared with the prepared inputs' one launch per token)
-        ot_us = one_token["us_per_token"]
+        # (runs of tokens as with prepared inputs)
         prep = {"us_per_token": round(prep_us, 2), "tokens": n,
-                "over_prepared_inputs_us": round(prep_us - ot_us, 2),
-                "kernels": "producers inside k_decode_tok (one launch per token; q rows "
-                           "prepared in LDS, fresh k by the tail waves)"}
+                "over_prepared_inputs_us": round(prep_us - us_tok, 2),
+                "kernels": "producers inside k_decode_tok (runs of tokens; q rows prepared "
+                           "in LDS, fresh k by the tail waves, each token's RoPE by the "
+                           "control wave)"}
         log(f"decode with fused QK producers: {prep_us:.2f} us/token "
-            f"({prep_us - ot_us:+.2f} against prepared inputs, one launch per token)")
+            f"({prep_us - us_tok:+.2f} against prepared inputs)")
 
     # ---- the whole attention branch (engine.cu:792-859): INT4 q/k/v in one
     # launch, producers + attention, out_proj into the residual; synthetic

@@ -70,7 +70,8 @@ constexpr int tML = tO + (kFpWaves + 1) * GQA * D * 4;      // f32x2 [9][4]
 constexpr int tX = (tML + (kFpWaves + 1) * GQA * 8 + 127) / 128 * 128;  // extra wave: K, V tile
 constexpr int tXS = tX + 2 * kTileB;                        // extra wave: [2 slots][K, V][kScaleB]
 constexpr int tSC = tXS + 4 * kScaleB;                     // f32 [2][64]: RoPE sin, cos per lane
-constexpr int tBytes = tSC + 2 * D * 4;
+constexpr int tINV = tSC + 2 * D * 4;                       // f32 [64]: RoPE inverse frequency per lane
+constexpr int tBytes = tINV + D * 4;
 static_assert(tBytes <= 160 * 1024, "LDS");
 
 // Timeline build (-DCIA_TIMELINE, `make TIMELINE=1`): each wave keeps up to
@@ -165,20 +166,29 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
   const int np = r <= ne ? kFpWaves + 1 : kFpWaves;         // wave partials in LDS
   const float qscale = a.scale * kLog2e;
   const int nl = a.nl, qpos = a.qpos, committed = a.committed;
-  // steps: token tok's layer li is step tok * nl + li (one token with the
-  // producers: their rotation is per position)
-  const int ntok = kPrep ? 1 : a.ntok, ns = ntok * nl;
+  // steps: token tok's layer li is step tok * nl + li
+  const int ntok = a.ntok, ns = ntok * nl;
   // the step each wave is at (its role loop sets them): token, tail keys
   // of the token (the fresh one last) and step
   int tok = 0, tt = qpos + 1 - committed, step = 0;
 
-  // ---- control wave: the RoPE rotation of lane l at qpos (the same for
-  // every layer) into LDS for the waves that prepare rows, and the zero row
-  // of the block-diagonal Q^T (both read after B1 of layer 0)
+  // ---- control wave: the RoPE rotation of lane l at a token's position
+  // (the same for every layer of the token) into LDS for the waves that
+  // prepare rows, and the zero row of the block-diagonal Q^T (both read
+  // after B1 of layer 0).  The first token's here; each later token's by
+  // the control loop once the token before has passed B3, from the inverse
+  // frequencies kept in LDS.
   float* ssc = (float*)(lds + tSC);
+  float* sinv = (float*)(lds + tINV);
+  auto rope_rows = [&](int pos) __attribute__((always_inline)) {
+    float sn, cs;
+    rope_sincos_f(sinv[l], pos, sn, cs);
+    ssc[l] = sn;
+    ssc[D + l] = cs;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // (written before the barrier the readers pass)
+  };
   if (w == kCtlW) {
     if constexpr (kPrep) {
-      float sn, cs;
       float invf = 0.f;
 #pragma unroll
       for (int k = 0; k < D / 2; k++) {
@@ -186,9 +196,8 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
             float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a.rt.invf[k])));
         invf = (l & 31) == k ? fk : invf;
       }
-      rope_sincos_f(invf, qpos, sn, cs);
-      ssc[l] = sn;
-      ssc[D + l] = cs;
+      sinv[l] = invf;
+      rope_rows(qpos);
     }
     sq[GQA * D + l] = 0;
   }
@@ -782,8 +791,8 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
   // tokens without a commit between them; only the last may commit).
   if (fp8w) {
     for (int st = 0; st < ns; st++) {
-      tok = kPrep ? 0 : st / nl;
-      const int li = kPrep ? st : st - tok * nl;
+      tok = st / nl;
+      const int li = st - tok * nl;
       step = st;
       b0();
       b1();
@@ -802,12 +811,17 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // (nothing left in flight)
   } else if (w == kCtlW) {
     for (int st = 0; st < ns; st++) {
-      tok = kPrep ? 0 : st / nl;
-      const int li = kPrep ? st : st - tok * nl;
+      tok = st / nl;
+      const int li = st - tok * nl;
       step = st;
       if (st > 0) control_wait(li);
-      if constexpr (kPrep)
+      if constexpr (kPrep) {
+        // a new token: its rotation (every wave has passed B3 of the token
+        // before, so that token's reads are done; B0 orders the writes
+        // before the next reads)
+        if (li == 0 && st > 0) rope_rows(qpos + tok);
         prep_part(li);
+      }
       else
         open_rows(li, 0, GQA, true);
       b1();
@@ -837,24 +851,17 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
         b3();
       }
     };
-    if constexpr (kPrep) {
-      if (tt == G)
-        tail_loop(T_{});
-      else
-        tail_loop(F_{});
-    } else {
-      // (only the last token may fill the group)
-      for (tok = 0; tok < ntok; tok++) {
-        tt = qpos + tok + 1 - committed;
-        if (tt == G) break;
-        tail_loop(F_{});
-      }
-      if (tok < ntok) tail_loop(T_{});
+    // (only the last token may fill the group)
+    for (tok = 0; tok < ntok; tok++) {
+      tt = qpos + tok + 1 - committed;
+      if (tt == G) break;
+      tail_loop(F_{});
     }
+    if (tok < ntok) tail_loop(T_{});
   } else {
     for (int st = 0; st < ns; st++) {
-      tok = kPrep ? 0 : st / nl;
-      const int li = kPrep ? st : st - tok * nl;
+      tok = st / nl;
+      const int li = st - tok * nl;
       step = st;
       prep_part(li);
       b1();
@@ -939,13 +946,14 @@ extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok_fits(const c
 // rows).  Token t + 1's layer 0 is scored after token t's last layer's
 // output is stored, as layer j + 1 after layer j.  Only the last token may
 // fill the group (the caller splits its runs there: the groups of the FP8
-// waves stay the same), and ntok > 1 needs prepared q / k (no producers:
-// their rotation is per position).  The workspace is layer 0's ws_decode.
+// waves stay the same).  With the producers the control wave writes each
+// token's rotation before the token's first layer opens.  The workspace is
+// layer 0's ws_decode.
 extern "C" __attribute__((visibility("hidden"))) int cia_decode_tok(
     const cia_layer* L, int nl, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     uint16_t* out, int past, float scale, int ntok, int64_t qs, int64_t kvs, void* stream) {
   if (!q || !k || !v || !out) return CIA_ERR_NULL;
-  if (ntok < 1 || ntok > G || (ntok > 1 && L[0].qw)) return CIA_ERR_ARG;
+  if (ntok < 1 || ntok > G) return CIA_ERR_ARG;
   if (!aligned(q, 2) || !aligned(k, 2) || !aligned(v, 2) || !aligned(out, 2)) return CIA_ERR_ALIGN;
   const int committed = L[0].committed, ng = committed / G, R = dec_ranges(ng);
   if (ntok > 1) {

@@ -356,10 +356,10 @@ extern "C" int cia_decode_loop_runs(cia_layer* layers, int n_layers, const uint1
   for (int i = 0; i < steps; i++) {
     const int pos = past + i;
     // A run of steps (at most tok_max) in one launch when every layer of a
-    // step goes in one launch, no per-step events are asked for and q / k
-    // come prepared: the steps up to the one that fills the group (it ends
-    // the run; the next run's FP8 groups include it).
-    if (!events && per > 1 && n_layers <= per && !layers[0].qw && tok_max > 1) {
+    // step goes in one launch and no per-step events are asked for: the
+    // steps up to the one that fills the group (it ends the run; the next
+    // run's FP8 groups include it).
+    if (!events && per > 1 && n_layers <= per && tok_max > 1) {
       const int run = decode_run(layers, n_layers, pos, std::min(steps - i, tok_max));
       if (run > 1) {
         const size_t r = (size_t)i * n_layers;

@@ -451,11 +451,12 @@ int cia_decode_loop(cia_layer* layers, int n_layers, const uint16_t* q,
  * In one launch layer l + 1's scores start only after every output row of
  * layer l is stored (its q would be computed from them), while its FP8 K/V
  * already stream in; outputs and cache bytes are bit-identical to the
- * per-layer launches.  When all the layers of a step go in one launch, no
- * events are given and q / k come prepared (no QK producers), consecutive
- * steps run in that same launch too, up to the step whose token fills a
- * group (a run of at most 64 steps): step t + 1's first layer is scored only
- * after step t's last layer has stored its output, as between layers.  The
+ * per-layer launches.  When all the layers of a step go in one launch and no
+ * events are given, consecutive steps run in that same launch too, up to
+ * the step whose token fills a group (a run of at most 64 steps): step
+ * t + 1's first layer is scored only after step t's last layer has stored
+ * its output, as between layers (with the QK producers, each step's RoPE at
+ * its own position).  The
  * workspace is the first layer's ws_decode.  With events, every step is a
  * launch of its own, and every layer of such a launch has events[3r]
  * recorded before it and events[3r+1], events[3r+2] after it.  The

@@ -20,7 +20,8 @@ oracle:
   consecutive tokens up to the one that fills a group) against one launch
   per token and against runs of at most 5 tokens: the same cache bytes and
   bit-identical outputs, through group commits, at 4155, 32 763, 40 000,
-  65 600 and 131 000 keys;
+  65 600 and 131 000 keys, and with the QK producers inside at 4155 and
+  32 763 keys;
 - the workspace's fault word stays 0 (no bounded wait gave up).
 """
 import ctypes
@@ -247,18 +248,41 @@ def test_runs_match_one_token_launches(cia, dev, n0, nL, steps):
     step bit-identical, and the fault word 0.  A run only moves launch
     boundaries; each step's arithmetic is the same.  At 131 000 keys the
     FP8 waves take several units each and the head pairs unequal ranges."""
-    from cuda_inf_amd import _lib
-    print(f"runs vs one token per launch: {n0} keys, {nL} layers, {steps} steps", flush=True)
+    _runs_vs_one_token(dev, n0, nL, steps, False)
+
+
+@pytest.mark.parametrize("n0,nL,steps", [(4155, 6, 70), (32763, 3, 12)])
+def test_runs_with_producers_match_one_token_launches(cia, dev, n0, nL, steps):
+    """The same with the QK producers inside the kernel (raw q / k): in a
+    run the control wave writes each token's rotation before the token's
+    first layer opens."""
+    _runs_vs_one_token(dev, n0, nL, steps, True)
+
+
+def _runs_vs_one_token(dev, n0, nL, steps, producers):
+    from cuda_inf_amd import _lib, workload
+    print(f"runs vs one token per launch: {n0} keys, {nL} layers, {steps} steps, "
+          f"producers={producers}", flush=True)
     maxT = n0 + steps + 64
     g = np.random.default_rng(31 + n0)
     q = (g.standard_normal((steps, nL, 32, 64)) * 2).astype(np.float16)
     k = (g.standard_normal((steps, nL, 8, 64)) * 2).astype(np.float16)
     v = g.standard_normal((steps, nL, 8, 64)).astype(np.float16)
     qd, kd, vd = _t16(q, dev), _t16(k, dev), _t16(v, dev)
+    qw = _t16(g.uniform(0.5, 1.5, 64).astype(np.float16), dev)
+    kw = _t16(g.uniform(0.5, 1.5, 64).astype(np.float16), dev)
     runs = []
     for tpl in (1, 0, 5):
         layers = _layers(dev, n0, nL, 800, maxT)
         arr = (_lib.cia_layer * nL)(*[L._s for L in layers])
+        keep = []
+        if producers:
+            for l in range(nL):
+                pw = torch.zeros((32 + 8) * 64, dtype=torch.float16, device=dev)
+                keep.append(pw)
+                arr[l].qw, arr[l].kw = qw.data_ptr(), kw.data_ptr()
+                arr[l].eps, arr[l].theta = workload.EPS, workload.ROPE_THETA
+                arr[l].prep_ws, arr[l].prep_cap = pw.data_ptr(), 1
         out = torch.zeros((steps, nL, 32, 64), dtype=torch.float16, device=dev)
         _lib.call("cia_decode_loop_runs", arr, nL, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
                   out.data_ptr(), n0, steps, 0.125, 0, tpl, None,
