@@ -206,7 +206,11 @@ def main():
     ev_arr = (ctypes.c_void_p * nev)(*[e.cuda_event for e in evs]) if nev else None
     run(K, ev_arr)
     torch.cuda.synchronize()
-    one = sorted(evs[3 * nL * r].elapsed_time(evs[3 * nL * r + 1]) * 1e3 for r in range(K))
+    # the loop records each layer's "before" event ahead of the launch and its
+    # "after" events behind it: the last "before" (layer nL-1) and the first
+    # "after" (layer 0) bracket the launch alone
+    one = sorted(evs[3 * nL * r + 3 * (nL - 1)].elapsed_time(evs[3 * nL * r + 1]) * 1e3
+                 for r in range(K))
     ev_us = one[len(one) // 2]
     log(f"decode launches: {n_launch} for {K} tokens, {dec_us:.2f} us and {dec_bytes / 1e6:.2f} MB "
         f"each, {achieved:.0f} GB/s; one token per launch (event-bracketed): median {ev_us:.2f} us")
