@@ -1,10 +1,14 @@
-// decode_tok.hip -- flash-decoding of one token through up to 8 attention
-// layers in ONE launch: per layer the reference runs attn_decode_split ->
-// attn_decode_combine (engine.cu:846-852) after the fresh token's tail write
-// and, when the token fills the group, its commit (engine.cu:190-228,
-// 830-845).  The layers of one step share their context length, so one
-// grid serves them all and layer l + 1's FP8 K and V stream into LDS while
-// layer l's partials merge across the chip.
+// decode_tok.hip -- flash-decoding of a run of consecutive tokens through
+// up to 8 attention layers each, in ONE launch: per layer the reference
+// runs attn_decode_split -> attn_decode_combine (engine.cu:846-852) after
+// the fresh token's tail write and, when the token fills the group, its
+// commit (engine.cu:190-228, 830-845).  The layers of one step share their
+// context length, so one grid serves them all and layer l + 1's FP8 K and V
+// stream into LDS while layer l's partials merge across the chip.  The
+// tokens of a run up to the one that fills the group keep the same FP8
+// groups, so the run's steps (token, layer) go in order through the same
+// grid, and the last layer of token t hands over to layer 0 of token t + 1
+// as one layer to the next.
 //
 // Work split.  As in the one-layer decode (decode_kv.hip): workgroup =
 // (kv head g, key range r), 8R workgroups (one per CU, all resident), the
@@ -787,8 +791,8 @@ __global__ __launch_bounds__(kTokThreads) void k_decode_tok(TokArgs a) {
     }
   };
   // Each role's loop runs the steps in order: token tok = st / nl, layer
-  // li = st % nl (one token per launch but in the decode loop's runs of
-  // tokens without a commit between them; only the last may commit).
+  // li = st % nl (a run of tokens without a commit between them; only the
+  // last token may commit).
   if (fp8w) {
     for (int st = 0; st < ns; st++) {
       tok = st / nl;
