@@ -211,8 +211,13 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv_int4(GemvArgs a) {
 //   choosing which global chunk each lane fetches), in a ring of 3 slots
 //   filled two groups ahead: per group one wait for the group's own DMA,
 //   one barrier, and no staging registers.
-//     X slot: 128 rows x 16 chunks; row r's chunk c at c ^ (r & 15) (the 16
-//       rows of an MFMA read hit distinct banks).
+//     X slot: 128 rows x 16 chunks; row r's chunk c at c ^ xsw(r).  A
+//       16-byte read is served 32 lanes (512 bytes of banks) at a time:
+//       lanes 16q + n (q = 0, 1 or 2, 3) read row n's chunks 4q + s, and
+//       two rows of one parity share a 512-byte bank window, so xsw maps
+//       the 8 rows of a parity to distinct offsets whose bit 2 is the
+//       parity: chunk 4q + s of one q and of the other never land on one
+//       bank (and the 16 rows of a read take 16 distinct offsets).
 //     W slot: 128 columns x 4 chunks of nibbles; column c's chunk q at
 //       q ^ ((c >> 2) & 3) (16 consecutive columns hit distinct banks).
 //     scale slot: the 128 columns' fp16 scales of the group, one per dword
@@ -226,6 +231,10 @@ constexpr int kSSlot = 2 * kTile * 4;          // bytes: 128 scale dwords + a dr
 constexpr int kSlot = kXSlot + kWSlot + kSSlot;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+// X slot chunk swizzle of row r: bits 1-2 of r to bits 0-1, bit 0 to bit 2,
+// bit 3 stays
+__device__ __forceinline__ int xsw(int r) { return ((r >> 1) & 3) | ((r & 1) << 2) | (r & 8); }
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
 // 8 nibbles (one u32, k even in the low nibble) -> 8 fp16 (nibble - 8), in k order
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemvArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; t++) {
     const int r = 4 * (4 * w + t) + (l >> 4), m = m0 + r;
-    const int lc = (l & 15) ^ (r & 15);
+    const int lc = (l & 15) ^ xsw(r);
     xsrc[t] = (const uint8_t*)(a.x + (size_t)(m < a.M ? m : a.M - 1) * K) + 16 * lc;
   }
   //   W: wave w fills columns 16 w .. +15; lane l takes column 16 w + (l >> 2),
@@ -335,7 +344,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int r = 64 * wm + 16 * i + n16;
-        A[i] = *(const f16x8*)(xs + r * 128 + 8 * ((4 * q + s2) ^ n16));
+        A[i] = *(const f16x8*)(xs + r * 128 + 8 * ((4 * q + s2) ^ xsw(n16)));
       }
 #pragma unroll
       for (int j = 0; j < 2; j++) B[j] = nib8(wq[j][s2]);
