@@ -121,6 +121,12 @@ __device__ __forceinline__ int wave_id() {
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2_t;
 
+// piece swizzle of V row r in LDS (4 pieces of 16 bytes per 64-byte row): a
+// read of rows 8k + j (k = 0..3, j = 0..7) is served 32 lanes (512 bytes of
+// banks) or 16 lanes at a time; bit 0 = bit 2 ^ bit 4 of r and bit 1 = bit
+// 3 make the rows that share banks in either grouping take distinct pieces
+__device__ __forceinline__ int vsw(int r) { return (((r >> 2) ^ (r >> 4)) & 1) | ((r >> 2) & 2); }
+
 // ds_read_b64_tr_b8: within each 16-lane block, lane i receives byte i mod 8
 // of the 8-byte rows addressed by lanes 2j + (i div 8), j = 0..7
 __device__ __forceinline__ u32x2 lds_read_tr8(const uint8_t* p) {
@@ -142,7 +148,10 @@ __device__ __forceinline__ f16x8 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
 // memory once.  kPlace (Sq = 1): the token is placed here (H2oPlace).
 template <bool kPlace>
 __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
-  __shared__ __attribute__((aligned(16))) uint8_t vl[64 * D];  // V rows of the block's slots, this kv head
+  // V rows of the block's slots, this kv head: row r's 16-byte piece c at
+  // c ^ vsw(r), so the transposing reads of 32 rows (one piece each) hit
+  // distinct banks
+  __shared__ __attribute__((aligned(16))) uint8_t vl[64 * D];
   __shared__ __attribute__((aligned(16))) _Float16 wl[GQA][64];  // each head's numerators (fp16)
   __shared__ __attribute__((aligned(16))) _Float16 vsl[64];      // the slots' V scales
   __shared__ __attribute__((aligned(16))) uint8_t newkv[2][D];  // kPlace: the token's K / V bytes
@@ -260,7 +269,7 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
       if (t0 + row == slot) vst = *(const u32x4*)(newkv[1] + 16 * c4);
     }
   }
-  *(u32x4*)(vl + row * D + c4 * 16) = vst;
+  *(u32x4*)(vl + row * D + 16 * (c4 ^ vsw(row))) = vst;
   const bool ok = live && sp <= qpos;
   float s = kNegInf;
   if (ok) {
@@ -309,7 +318,8 @@ __global__ __launch_bounds__(256) void k_h2o_scores(H2oArgs a, H2oPlace pl) {
     const f16x8 sc8 = *(const f16x8*)&vsl[sl0];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
-      const u32x2 raw = lds_read_tr8(vl + (sl0 + (ln >> 1)) * D + 16 * dt + 8 * (ln & 1));
+      const int vr = sl0 + (ln >> 1);
+      const u32x2 raw = lds_read_tr8(vl + vr * D + 16 * (dt ^ vsw(vr)) + 8 * (ln & 1));
       const f16x8 vb = e4m3x8_to_f16(raw[0], raw[1]) * sc8;
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, vb, acc[dt], 0, 0, 0);
     }
